@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the FP8 projection path on one MI355X.
+
+    python bench.py [--config C2] [--steps K] [--warmup W] [--no-cpu] [--no-others]
+
+A "step" is one pass of the hot path over one batch of synthetic input:
+per-token quantization of every projection input, the FP8 GEMMs with fused
+epilogues, and the re-quantization of GELU/GLU outputs. The headline workload is
+BASELINE configs[1] (C2: GR00T-style DiT action head, M=16, 4 flow-matching
+steps per timed unit), reported in GB/s of algorithmic HBM traffic; C1, C3, C4
+and C5 are measured in the same run and reported under "configs".
+
+Timing: K steps are captured into one HIP graph (inputs already resident in HBM,
+weights rotating through a pool larger than the 256 MB Infinity Cache for
+M <= 64) and replayed once between synchronizations, after W warm-up steps.
+The dominant kernel's average duration is measured separately with HIP events
+around a graph of back-to-back launches of that kernel alone, on the stream it
+runs on, and gives the "roofline" object.
+
+The CPU baseline runs the reference's PyTorch CPU FP8 path (oracle/cpu_path.py)
+on the host cores for one C2 unit.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, TFLOP/s
+METRIC = "FP8 linear TFLOP/s (% of MI355X FP8 MFMA peak) + GB/s for M<=64; p50 us/call"
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def capture(fn, n, stream):
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(n):
+            fn(i)
+    return g
+
+
+def time_graph(g, reps=1):
+    """Replay g `reps` times; returns (event ms, wall ms) over all replays."""
+    import torch
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return e0.elapsed_time(e1), (t1 - t0) * 1e3
+
+
+def measure(wl, steps, warmup, kernel_launches=64):
+    """Returns per-step and dominant-kernel timings of one workload."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # eager warm-up on the capture stream (workspaces, code objects)
+        for _ in range(2):
+            wl.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gw = capture(lambda i: wl.step(), max(warmup, 1), side)
+    gk = capture(lambda i: wl.step(), steps, side)
+    gd = capture(lambda i: wl.dominant_call(i), kernel_launches, side)
+    time_graph(gw)
+    ev_ms, wall_ms = time_graph(gk)
+    time_graph(gd)  # warm
+    samples = [time_graph(gd)[0] / kernel_launches for _ in range(5)]
+    samples.sort()
+    kern_ms = samples[len(samples) // 2]
+    return dict(step_ms=ev_ms / steps, wall_step_ms=wall_ms / steps, kernel_ms=kern_ms)
+
+
+def summarize(wl, m):
+    step_s = m["step_ms"] * 1e-3
+    d = wl.dominant_gemm
+    k_s = m["kernel_ms"] * 1e-3
+    res = {
+        "title": wl.title,
+        "bound": wl.bound,
+        "us_per_step": round(m["step_ms"] * 1e3, 3),
+        "tflops": round(wl.flops / step_s / 1e12, 2),
+        "gbs": round(wl.bytes / step_s / 1e9, 1),
+        "gemm_gflop_per_step": round(wl.flops / 1e9, 3),
+        "bytes_per_step": wl.bytes,
+        "dominant": {
+            "kernel": f"{d.name} {d.M}x{d.N}x{d.K}" + (f" {d.act}" if d.act else ""),
+            "us": round(m["kernel_ms"] * 1e3, 3),
+            "tflops": round(d.flops / k_s / 1e12, 2),
+            "gbs": round(d.bytes / k_s / 1e9, 1),
+            "frac_mfma": round(d.flops / k_s / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "frac_hbm": round(d.bytes / k_s / 1e9 / HBM_PEAK_GBS, 4),
+        },
+    }
+    res["frac_step"] = round(res["gbs"] / HBM_PEAK_GBS, 4) if wl.bound == "hbm" else \
+        round(res["tflops"] / FP8_PEAK_TFLOPS, 4)
+    return res
+
+
+def cpu_baseline(seconds_hint=True):
+    """Reference CPU FP8 path for one C2 unit (4 flow steps = 8 projections)."""
+    import torch
+    from oracle import cpu_path
+    from instinctflash_amd.workloads import C2, Gemm, quant_bytes
+    g = torch.Generator().manual_seed(0)
+    M, D, FF = 16, 1536, 6144
+    xs = [torch.randn((M, D), generator=g).to(torch.bfloat16) for _ in range(4)]
+    w1 = torch.randn((FF, D), generator=g) * 0.02
+    w2 = torch.randn((D, FF), generator=g) * 0.02
+    res = torch.randn((M, D), generator=g).to(torch.bfloat16)
+    q1, s1 = cpu_path.quant_rows(w1)
+    q2, s2 = cpu_path.quant_rows(w2)
+    t0 = time.perf_counter()
+    cpu_path.c2_unit(xs, q1, s1, q2, s2, res)
+    dt = time.perf_counter() - t0
+    gemms = [Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True)]
+    nbytes = 4 * (sum(x.bytes for x in gemms) + quant_bytes(M, D) + quant_bytes(M, FF))
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds": round(dt, 2),
+            "sample": "one full C2 unit (4 flow steps x [quant, 16x1536->6144 GELU, quant, 16x6144->1536 +res]) "
+                      "via torch._scaled_mm (oneDNN) on the host CPU, reference GI decomposition",
+            "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the FP8 projection path has no multi-GPU step in this build "
+              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from instinctflash_amd import _lib
+    from instinctflash_amd.workloads import CONFIGS
+    if not torch.cuda.is_available():
+        print("bench.py needs the MI355X GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    dev = torch.device("cuda:0")
+    arch = torch.cuda.get_device_properties(0).gcnArchName
+
+    results = {}
+    order = [args.config] + ([] if args.no_others else [k for k in CONFIGS if k != args.config])
+    for key in order:
+        wl = CONFIGS[key](dev)
+        steps = args.steps if key == args.config else max(10, min(args.steps, 20))
+        _log(f"[bench] {key}: {wl.title} (pool {wl.pool}, {steps} steps)")
+        m = measure(wl, steps, args.warmup)
+        results[key] = summarize(wl, m)
+        results[key]["steps"] = steps
+        if key == args.config:
+            head = (wl, m)
+        del wl
+        torch.cuda.empty_cache()
+
+    wl, m = head
+    r = results[args.config]
+    d = wl.dominant_gemm
+    k_s = m["kernel_ms"] * 1e-3
+    if wl.bound == "hbm":
+        value, unit = r["gbs"], "GB/s"
+        roof = {"bound": "hbm", "achieved": round(d.bytes / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        value, unit = r["tflops"], "TFLOP/s"
+        roof = {"bound": "mfma", "achieved": round(d.flops / k_s / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
+                "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    roof["kernel"] = r["dominant"]["kernel"]
+    roof["kernel_us"] = r["dominant"]["us"]
+
+    out = {
+        "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(m["step_ms"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 x fp8-e4m3 -> fp32 acc, bf16 out",
+        "data": "synthetic (seeded torch.Generator on CPU, random-init weights quantized per channel)",
+        "config": {"workload": f"{args.config}: {wl.title}", "M": d.M, "gpu": arch,
+                   "timed_unit": "4 flow-matching steps" if wl.steps_per_unit > 1 else "one pass"},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        _log("[bench] CPU baseline (reference CPU FP8 path, one C2 unit)")
+        out["cpu_baseline"] = cpu_baseline()
+    out["configs"] = results
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/*
+ * ifx_fp8.h -- C ABI of the MI355X (gfx950) FP8 projection path.
+ *
+ * One shared library (libifx_fp8.so) exports these entry points. Every pointer
+ * argument is a DEVICE pointer except where noted; `stream` is a hipStream_t
+ * (NULL = the null stream). No entry point allocates memory, synchronises the
+ * host, or keeps mutable global state: the caller owns every buffer, so a call
+ * may be captured into a HIP graph. Calls on distinct streams are independent,
+ * except that a workspace buffer must not be shared by calls that may overlap.
+ *
+ * Return value: IFX_OK (0), a negative IFX_ERR_* for an argument the library
+ * rejects before launching anything, or a positive hipError_t from the launch.
+ *
+ * Data formats
+ *   e4m3  : OCP FP8 E4M3FN bytes (torch.float8_e4m3fn), NaN = 0x7F/0xFF.
+ *   bf16  : bfloat16 bit patterns.
+ *   scale : float32. Row m of a quantized tensor dequantizes as q[m,:] * scale[m].
+ *   Strides (ld*) are in ELEMENTS of the tensor they describe.
+ *
+ * The quantization recipe (reference: instinctflash/kernels/fp8.py:30-37, with
+ * the device scalar-division semantics pinned by instinctflash/runtime/
+ * fp8_pack.py:83-91 and tests/test_sm89_fp8.py:48-56) is, per row m:
+ *   amax[m]  = max_k |x[m,k]|            (NaN if any element is NaN)
+ *   scale[m] = max(amax[m], 1e-12f) * fl32(1/448)
+ *   q[m,k]   = e4m3_rne(clamp(x[m,k] / scale[m], -448, 448))   (IEEE division)
+ */
+#ifndef IFX_FP8_H
+#define IFX_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFX_ABI_VERSION 1
+
+/* status codes (negative = rejected before launch) */
+#define IFX_OK 0
+#define IFX_ERR_INVALID (-1)     /* a size, stride or flag is out of contract   */
+#define IFX_ERR_ALIGN (-2)       /* a pointer/stride breaks 16-byte alignment    */
+#define IFX_ERR_WORKSPACE (-3)   /* workspace missing or smaller than required   */
+#define IFX_ERR_UNSUPPORTED (-4) /* shape not supported by any kernel variant    */
+
+/* source dtypes for the quantizers */
+#define IFX_DTYPE_BF16 0
+#define IFX_DTYPE_F32 1
+
+/* activation selector for gated_act_quant (reference kernels/activation.py:15-16) */
+#define IFX_ACT_GELU_TANH 0
+#define IFX_ACT_SILU 1
+
+/* fp8_linear epilogue flags (bitmask). Evaluation order per output element:
+ *   y = acc[m,n] * sa[m] * sw[n]                     (sa / sw NULL => 1)
+ *   y = y + bias[n]                                  IFX_EPI_BIAS
+ *   y = gelu_tanh(y)                                 IFX_EPI_GELU_TANH
+ *   h = act(y_gate) * y_up                           IFX_EPI_GEGLU / IFX_EPI_SWIGLU
+ *       (weights packed with gate/up rows interleaved in blocks of 16, output
+ *        width N/2; see ifx_fp8_pack_glu)
+ *   y = y * gate[n]                                  IFX_EPI_GATE   (adaLN gate, bf16 [N_out])
+ *   y = residual[m,n] + y                            IFX_EPI_RESIDUAL
+ *   out[m,n] = round(y)                              bf16, or f32 with IFX_EPI_OUT_F32
+ * residual is bf16 unless IFX_EPI_RES_F32. out may alias residual (in-place update).
+ */
+#define IFX_EPI_NONE 0
+#define IFX_EPI_BIAS 1
+#define IFX_EPI_GELU_TANH 2
+#define IFX_EPI_GEGLU 4
+#define IFX_EPI_SWIGLU 8
+#define IFX_EPI_RESIDUAL 16
+#define IFX_EPI_GATE 32
+#define IFX_EPI_OUT_F32 64
+#define IFX_EPI_RES_F32 128
+
+int ifx_abi_version(void);
+/* Host pointer to a static string describing a status code. */
+const char* ifx_status_string(int status);
+
+/*
+ * Per-row dynamic quantization of x [M,K] (bf16 or f32) to e4m3 q [M,K] and
+ * scale [M] with the recipe above.
+ * Replaces: the activation quantizer the engines run before every FP8 GEMM
+ * (reference instinctflash/kernels/norm.py:127-158 `row_quant`, recipe of
+ * kernels/fp8.py:30-37) and, with IFX_DTYPE_F32, `quantize_weight`'s per-output-
+ * channel pass (kernels/fp8.py:30-37; rows = output channels).
+ */
+int ifx_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                   void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * Whole-tensor (per-tensor) dynamic quantization of a contiguous bf16 tensor of
+ * `count` elements: one scale for all elements, same recipe, NaN anywhere =>
+ * NaN scale. `partial` is a caller-provided device workspace of
+ * ifx_quant_tensor_workspace_size(count) bytes.
+ * Replaces: instinctflash/runtime/fp8_pack.py:83-91 `dynamic_pack_bf16_e4m3`.
+ */
+size_t ifx_quant_tensor_workspace_size(int64_t count);
+int ifx_quant_tensor_bf16(const void* x, int64_t count, void* q, float* scale, void* partial,
+                          size_t partial_bytes, void* stream);
+
+/*
+ * Pack a contiguous bf16 tensor with a FIXED device scale (one f32 element):
+ * q[i] = e4m3_rne(clamp(x[i] / *scale, -448, 448)).
+ * Replaces: instinctflash/runtime/fp8_pack.py:48-60 `pack_bf16_e4m3`.
+ */
+int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void* q, void* stream);
+
+/*
+ * Consumer-side producer of the next FP8 operand from a raw bf16 accumulator:
+ *   v = x[m,k] * row[m] * col[k] + bias[k]   (NULL factors are skipped)
+ *   v = gelu_tanh(v) if gelu
+ *   (q[m,:], scale[m]) = quantize(v) with the recipe above (FP32 v, no bf16 rounding).
+ * Replaces: instinctflash/kernels/norm.py:150-158 `row_quant`.
+ */
+int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row,
+                  const float* col, const float* bias, int gelu, void* q, int64_t ldq,
+                  float* scale, void* stream);
+
+/*
+ * Gated activation + requantization from a raw bf16 gate|up accumulator gu [M,2F]:
+ *   g = gu[m,f]*row[m]*col[f], u = gu[m,F+f]*row[m]*col[F+f], h = act(g)*u
+ *   (q[m,:F], scale[m]) = quantize(h) with the recipe above.
+ * Replaces: instinctflash/kernels/activation.py:46-56 `gated_act_quant`.
+ */
+int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row,
+                        const float* col, int act, void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * y[m,d] = x[m,d] * row[m] * col[d] + bias[d], x bf16, y bf16 or f32 (y_dtype).
+ * Replaces: instinctflash/kernels/norm.py:178-185 `dequant_rows`.
+ */
+int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const float* row,
+                     const float* col, const float* bias, void* y, int y_dtype, int64_t ldy,
+                     void* stream);
+
+/*
+ * FP8 x FP8 GEMM with fp32 accumulation and fused epilogue:
+ *   acc[m,n] = sum_k a[m,k] * w[n,k]      a e4m3 [M,K] (lda), w e4m3 [N,K] (ldw)
+ *   out = epilogue(acc)  (flags above; out [M, N_out], N_out = N/2 for GLU else N)
+ * Contract: N % 16 == 0 (N % 32 for GLU), K % 16 == 0, a/w/out 16-byte aligned,
+ * lda/ldw multiples of 16, ldo/ldr multiples of 8. sa: f32 [M] or NULL,
+ * sw: f32 [N] or NULL, bias: f32 [N] or NULL, gate: bf16 [N_out] or NULL.
+ * workspace: ifx_fp8_linear_workspace_size(M,N,K,epilogue) bytes (may be 0 =>
+ * NULL allowed). Its first 4096 bytes hold split-K tickets: zero-fill them once
+ * before the first use; every call leaves them zero again, whatever the shape,
+ * so one workspace serves any sequence of calls on one stream.
+ * With sa = sw = NULL and epilogue 0 this is the raw-accumulator GEMM of
+ * instinctflash/kernels/fp8.py:50-53 `gemm` (torch._scaled_mm with unit scales,
+ * bf16 out). With scales and flags it fuses the consumers
+ * kernels/norm.py:161-175 (dequant_rows), :45-58 (residual/gated residual),
+ * :135-144 (gelu), kernels/activation.py:26-40 (GeGLU/SwiGLU),
+ * kernels/rope.py:36-45 and kernels/wan.py:27-31 (rescale + bias).
+ */
+size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue);
+int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
+                   const float* sw, const float* bias, const void* residual, int64_t ldr,
+                   const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
+                   int64_t K, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Repack a gate|up weight (rows [0,F) gate, [F,2F) up; e4m3 [2F,K] + f32 scale
+ * [2F] + optional f32 bias [2F]) into the interleaved layout the GLU epilogue
+ * reads: packed rows 32j..32j+15 = gate rows 16j..16j+15, rows 32j+16..32j+31 =
+ * up rows 16j..16j+15. Device-to-device, F % 16 == 0. bias/bias_out may be NULL.
+ * Replaces: the weight layout `gated_act_quant` assumes (kernels/activation.py:24-25).
+ */
+int ifx_fp8_pack_glu(const void* w, const float* scale, const float* bias, int64_t F, int64_t K,
+                     void* w_out, float* scale_out, float* bias_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IFX_FP8_H */

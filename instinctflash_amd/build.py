@@ -1,0 +1,62 @@
+"""Build libifx_fp8.so (gfx950) in-tree with hipcc.
+
+    python -m instinctflash_amd.build          # compile and report
+
+The library is plain HIP C++ behind the C ABI of include/ifx_fp8.h; no torch
+headers are involved, so the build is a single hipcc invocation.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libifx_fp8.so"
+SOURCES = ("quant.hip", "gemm.hip")
+ARCH = "gfx950"
+
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # IEEE round-to-nearest FP32 division is part of the quantization recipe.
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # Keep FP32 denormals (bf16 subnormal inputs must quantize exactly).
+    "-fno-gpu-flush-denormals-to-zero",
+    # Packed-FP32 VALU forms are disabled on this platform.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 kernels cannot be built")
+
+
+def build(verbose: bool = False) -> Path:
+    srcs = [str(CSRC / s) for s in SOURCES]
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, f"-I{ROOT / 'include'}", *srcs, "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    path = build(verbose=True)
+    print(f"built {path}", file=sys.stderr)

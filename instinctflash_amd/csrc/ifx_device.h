@@ -1,0 +1,110 @@
+// Device-side helpers shared by the FP8 projection kernels (gfx950 only).
+//
+// * OCP E4M3FN encoding (bias 7, no infinities, 0x7F/0xFF = NaN, max finite 448)
+//   written from the OCP 8-bit floating point specification: round to nearest,
+//   ties to even, on the FP32 bit pattern.
+// * BF16 <-> FP32 bit helpers.
+// * MFMA fragment types for v_mfma_f32_{16x16x128,32x32x64}_f8f6f4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifx {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Largest finite E4M3FN magnitude.
+constexpr float kFp8Max = 448.0f;
+// The activation/weight scale is amax * fl32(1/448): this is how a device
+// division by a host scalar is evaluated (multiply by the FP32 reciprocal),
+// which the reference recipe relies on (instinctflash/runtime/fp8_pack.py:88-89,
+// tests/test_sm89_fp8.py:48-56). The constant is the correctly rounded FP32
+// reciprocal of 448.
+constexpr float kInvFp8Max = 1.0f / 448.0f;
+// Scale floor of the recipe (instinctflash/kernels/fp8.py:33 clamp_min(1e-12)).
+constexpr float kAmaxFloor = 1e-12f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// FP32 -> BF16 bits, round to nearest even; NaN stays NaN (quiet bit forced).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// FP32 -> E4M3FN byte, round-to-nearest-even.
+//  * |f| >= 2^-6 (normal range): keep 3 mantissa bits of the FP32 pattern with
+//    RNE, then rebias the exponent from 127 to 7 (127-7 = 120 -> 120<<3 = 960
+//    in the >>20 domain).
+//  * |f| <  2^-6: the E4M3 subnormal step is 2^-9, so the code is the integer
+//    RNE(|f| * 2^9); code 8 coincides with the smallest normal (exp 1, mant 0).
+//  * Magnitudes whose rounding leaves the finite range (above 464, the tie
+//    that rounds to even 448), infinities and NaN encode as NaN (0x7F) with the
+//    input's sign. Callers clamp finite inputs to +-448 first, so only NaN
+//    reaches that case.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  uint32_t code;
+  if (a >= 0x43F00000u) {            // >= 480.0 (incl. inf/NaN); (464,480) -> 0x7F below
+    code = 0x7Fu;
+  } else if (a >= 0x3C800000u) {     // >= 2^-6
+    code = ((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20) - 960u;
+  } else {
+    const uint32_t e = a >> 23;      // 0 .. 120
+    // value = m * 2^(e-150) for normal FP32 (m with implicit bit); we need
+    // RNE(value * 2^9) = RNE(m * 2^-(141-e)). FP32 subnormals and anything
+    // below 2^-11 round to zero.
+    if (e < 115u) {
+      code = 0u;
+    } else {
+      const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+      const uint32_t sh = 141u - e;  // 21 .. 26
+      code = (m + (1u << (sh - 1u)) - 1u + ((m >> sh) & 1u)) >> sh;
+    }
+  }
+  return code | sign;
+}
+
+// NaN-propagating clamp to [-448, 448] (a NaN input stays NaN).
+__device__ __forceinline__ float clamp_fp8(float v) {
+  return v != v ? v : fminf(fmaxf(v, -kFp8Max), kFp8Max);
+}
+
+// Wave-wide (64 lanes) max of an unsigned value.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    uint32_t o = __shfl_xor(v, off, 64);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715 x^3))), with tanh(u) = 1 - 2/(1+e^{2u}).
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // e^{2u}
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return 0.5f * x * (1.0f + t);
+}
+
+__device__ __forceinline__ float silu(float x) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);  // e^{-x}
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+}  // namespace ifx

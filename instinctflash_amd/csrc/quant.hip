@@ -1,0 +1,436 @@
+// Per-row (per-token / per-output-channel) and per-tensor dynamic FP8 E4M3
+// quantizers for gfx950, plus the consumer-side producers `row_quant`,
+// `gated_act_quant` and `dequant_rows`.
+//
+// Reference recipe: instinctflash/kernels/fp8.py:30-37 (quantize_weight), with
+// the device scale arithmetic of instinctflash/runtime/fp8_pack.py:83-91:
+//   scale = max(amax, 1e-12) * fl32(1/448),  q = e4m3_rne(clamp(x / scale, +-448))
+// The division is IEEE round-to-nearest (fp8_pack.py:32-34): this file must be
+// compiled with correctly rounded FP32 division (-fhip-fp32-correctly-rounded-
+// divide-sqrt, hipcc's default).
+//
+// Design (HBM-bound: 2-4 B read + 1 B written per element):
+//  * A "team" of T = 64/128/256 lanes owns one row; the row stays in registers
+//    (VPT 16-byte vectors per lane), so it is read from HBM exactly once.
+//  * The absmax reduction runs on |x| bit patterns as unsigned integers: for
+//    non-NaN floats that order equals the numeric order, and every NaN pattern
+//    compares above +inf (0x7F800000), so one integer max both finds amax and
+//    propagates NaN exactly as torch's amax does.
+//  * 128-bit loads, 64-bit stores of 8 packed E4M3 codes, scale written once.
+
+#include "ifx_abi.h"
+#include "ifx_device.h"
+
+// No multiply-add contraction in this file: the producers' FP32 arithmetic
+// (x*row*col + bias) must round after every operation, like the reference's
+// element-wise torch/numpy formulation, so the quantized bytes are reproducible.
+#pragma clang fp contract(off)
+
+namespace ifx {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4 r, float* v) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+
+// ---- row sources: produce 8 consecutive FP32 values of row m --------------
+
+struct SrcBf16 {
+  const uint16_t* x;
+  int64_t ldx;
+  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(x + m * ldx + k), v);
+  }
+  __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
+    return bf16_bits_to_f32(x[m * ldx + k]);
+  }
+};
+
+struct SrcF32 {
+  const float* x;
+  int64_t ldx;
+  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
+    const float4 a = *reinterpret_cast<const float4*>(x + m * ldx + k);
+    const float4 b = *reinterpret_cast<const float4*>(x + m * ldx + k + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ __forceinline__ float load1(int64_t m, int64_t k) const { return x[m * ldx + k]; }
+};
+
+// v = x*row[m]*col[k] + bias[k] (-> gelu_tanh); reference kernels/norm.py:135-144.
+struct SrcAffine {
+  const uint16_t* x;
+  int64_t ldx;
+  const float* row;
+  const float* col;
+  const float* bias;
+  int gelu;
+  __device__ __forceinline__ float op(float v, int64_t m, float c, float b) const {
+    if (row) v = v * row[m];
+    if (col) v = v * c;
+    if (bias) v = v + b;
+    if (gelu) v = gelu_tanh(v);
+    return v;
+  }
+  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(x + m * ldx + k), v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = op(v[i], m, col ? col[k + i] : 1.0f, bias ? bias[k + i] : 0.0f);
+  }
+  __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
+    return op(bf16_bits_to_f32(x[m * ldx + k]), m, col ? col[k] : 1.0f, bias ? bias[k] : 0.0f);
+  }
+};
+
+// h = act(g)*u from a gate|up accumulator; reference kernels/activation.py:26-40.
+struct SrcGated {
+  const uint16_t* gu;
+  int64_t ldgu;
+  int64_t F;
+  const float* row;
+  const float* col;
+  int act;
+  __device__ __forceinline__ float op(float g, float u, int64_t m, int64_t k) const {
+    if (row) {
+      const float r = row[m];
+      g = g * r;
+      u = u * r;
+    }
+    if (col) {
+      g = g * col[k];
+      u = u * col[F + k];
+    }
+    const float a = act == IFX_ACT_SILU ? silu(g) : gelu_tanh(g);
+    return a * u;
+  }
+  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
+    float g[8], u[8];
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(gu + m * ldgu + k), g);
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(gu + m * ldgu + F + k), u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = op(g[i], u[i], m, k + i);
+  }
+  __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
+    return op(bf16_bits_to_f32(gu[m * ldgu + k]), bf16_bits_to_f32(gu[m * ldgu + F + k]), m, k);
+  }
+};
+
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// scale from the max |x| bit pattern; NaN patterns (> +inf) give a NaN scale.
+__device__ __forceinline__ float scale_from_amax_bits(uint32_t amax_bits) {
+  if (amax_bits > 0x7F800000u) return __uint_as_float(0x7FC00000u);
+  return fmaxf(__uint_as_float(amax_bits), kAmaxFloor) * kInvFp8Max;
+}
+
+__device__ __forceinline__ uint32_t q1(float v, float s) { return f32_to_e4m3(clamp_fp8(v / s)); }
+
+// Team-wide max: lanes [team*T, team*T+T) of the block.
+template <int T>
+__device__ __forceinline__ uint32_t team_max(uint32_t v, uint32_t* red) {
+  v = wave_max_u32(v);
+  if constexpr (T > 64) {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const int first = (threadIdx.x / T) * (T / 64);
+    v = red[first];
+#pragma unroll
+    for (int i = 1; i < T / 64; ++i) v = v > red[first + i] ? v : red[first + i];
+  }
+  return v;
+}
+
+// Register-resident row quantizer: K % 8 == 0, 16-byte aligned rows,
+// ceil(K/8) <= T*VPT.
+template <int T, int VPT, class Src>
+__global__ __launch_bounds__(kBlock) void quant_rows_vec(Src src, int64_t M, int64_t K, uint8_t* q,
+                                                        int64_t ldq, float* scale) {
+  __shared__ uint32_t red[kBlock / 64];
+  constexpr int R = kBlock / T;
+  const int lt = threadIdx.x % T;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / T;
+  const bool row_ok = m < M;
+  const int64_t nvec = K >> 3;
+  float v[VPT][8];
+  uint32_t amax = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t idx = lt + static_cast<int64_t>(j) * T;
+    if (row_ok && idx < nvec) {
+      src.load8(m, idx * 8, v[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t b = abs_bits(v[j][i]);
+        amax = amax > b ? amax : b;
+      }
+    }
+  }
+  amax = team_max<T>(amax, red);
+  if (!row_ok) return;
+  const float s = scale_from_amax_bits(amax);
+  if (lt == 0) scale[m] = s;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int64_t idx = lt + static_cast<int64_t>(j) * T;
+    if (idx < nvec) {
+      uint2 o;
+      o.x = q1(v[j][0], s) | (q1(v[j][1], s) << 8) | (q1(v[j][2], s) << 16) | (q1(v[j][3], s) << 24);
+      o.y = q1(v[j][4], s) | (q1(v[j][5], s) << 8) | (q1(v[j][6], s) << 16) | (q1(v[j][7], s) << 24);
+      *reinterpret_cast<uint2*>(q + m * ldq + idx * 8) = o;
+    }
+  }
+}
+
+// Any K / alignment: one 256-lane block per row, two passes over the row.
+template <class Src>
+__global__ __launch_bounds__(kBlock) void quant_rows_generic(Src src, int64_t M, int64_t K,
+                                                            uint8_t* q, int64_t ldq, float* scale) {
+  __shared__ uint32_t red[kBlock / 64];
+  const int64_t m = blockIdx.x;
+  uint32_t amax = 0;
+  for (int64_t k = threadIdx.x; k < K; k += kBlock) {
+    const uint32_t b = abs_bits(src.load1(m, k));
+    amax = amax > b ? amax : b;
+  }
+  amax = team_max<kBlock>(amax, red);
+  const float s = scale_from_amax_bits(amax);
+  if (threadIdx.x == 0) scale[m] = s;
+  for (int64_t k = threadIdx.x; k < K; k += kBlock)
+    q[m * ldq + k] = static_cast<uint8_t>(q1(src.load1(m, k), s));
+}
+
+template <int T, int VPT, class Src>
+void launch_vec(const Src& src, int64_t M, int64_t K, uint8_t* q, int64_t ldq, float* scale,
+                hipStream_t st) {
+  constexpr int R = kBlock / T;
+  const int64_t grid = (M + R - 1) / R;
+  hipLaunchKernelGGL((quant_rows_vec<T, VPT, Src>), dim3(static_cast<unsigned>(grid)), dim3(kBlock),
+                     0, st, src, M, K, q, ldq, scale);
+}
+
+// Picks the register-resident variant (team size, vectors per lane) or falls
+// back to the two-pass kernel.
+template <class Src>
+int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
+                  float* scale, hipStream_t st) {
+  if (M == 0 || K == 0) {
+    if (M > 0 && K == 0) return IFX_ERR_INVALID;  // amax of an empty row is undefined
+    return IFX_OK;
+  }
+  if (M > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
+  const int64_t nvec = K / 8;
+  if (vec_ok && K % 8 == 0 && nvec <= 2048) {
+    if (nvec <= 64) launch_vec<64, 1>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 128) launch_vec<64, 2>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 256) launch_vec<64, 4>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 512) launch_vec<64, 8>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 1024) launch_vec<128, 8>(src, M, K, q, ldq, scale, st);
+    else launch_vec<256, 8>(src, M, K, q, ldq, scale, st);
+  } else {
+    hipLaunchKernelGGL((quant_rows_generic<Src>), dim3(static_cast<unsigned>(M)), dim3(kBlock), 0, st,
+                       src, M, K, q, ldq, scale);
+  }
+  return launch_status();
+}
+
+// ---- per-tensor quantizer (two launches, no host sync) --------------------
+
+constexpr int64_t kTensorChunk = 8192;  // elements per partial (one block)
+
+__global__ __launch_bounds__(kBlock) void tensor_amax_partial(const uint16_t* x, int64_t count,
+                                                             uint32_t* partial) {
+  __shared__ uint32_t red[kBlock / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTensorChunk;
+  uint32_t amax = 0;
+  for (int64_t i = base + threadIdx.x; i < base + kTensorChunk && i < count; i += kBlock) {
+    const uint32_t b = x[i] & 0x7FFFu;
+    amax = amax > b ? amax : b;
+  }
+  amax = team_max<kBlock>(amax, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = amax;
+}
+
+// Dynamic mode (partial != null): every block reduces the partials itself, so
+// no third launch is needed; block 0 writes the scale. Fixed mode: *scale is
+// read, not written (reference fp8_pack.py:48-60 pack_bf16_e4m3).
+__global__ __launch_bounds__(kBlock) void tensor_pack(const uint16_t* x, int64_t count,
+                                                     const uint32_t* partial, int64_t nparts,
+                                                     uint8_t* q, float* scale) {
+  __shared__ uint32_t red[kBlock / 64];
+  float s;
+  if (partial) {
+    uint32_t amax = 0;
+    for (int64_t i = threadIdx.x; i < nparts; i += kBlock) amax = amax > partial[i] ? amax : partial[i];
+    amax = team_max<kBlock>(amax, red);
+    // bf16 |x| bits -> f32 bits; NaN stays above +inf.
+    s = scale_from_amax_bits(amax << 16);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+  } else {
+    s = *scale;
+  }
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTensorChunk;
+  for (int64_t i = base + threadIdx.x; i < base + kTensorChunk && i < count; i += kBlock)
+    q[i] = static_cast<uint8_t>(q1(bf16_bits_to_f32(x[i]), s));
+}
+
+// ---- dequant_rows / GLU weight repack --------------------------------------
+
+__global__ __launch_bounds__(kBlock) void dequant_rows_kernel(const uint16_t* x, int64_t ldx,
+                                                             int64_t M, int64_t D, const float* row,
+                                                             const float* col, const float* bias,
+                                                             void* y, int y_f32, int64_t ldy) {
+  const int64_t m = blockIdx.y;
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (d >= D) return;
+  float v = bf16_bits_to_f32(x[m * ldx + d]);
+  if (row) v = v * row[m];
+  if (col) v = v * col[d];
+  if (bias) v = v + bias[d];
+  if (y_f32) static_cast<float*>(y)[m * ldy + d] = v;
+  else static_cast<uint16_t*>(y)[m * ldy + d] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+}
+
+// One block per packed row p: source row = gate or up row per the 16-row interleave.
+__global__ __launch_bounds__(kBlock) void pack_glu_kernel(const uint8_t* w, const float* scale,
+                                                         const float* bias, int64_t F, int64_t K,
+                                                         uint8_t* wo, float* so, float* bo) {
+  const int64_t p = blockIdx.x;
+  const int64_t j = (p >> 5) * 16 + (p & 15);
+  const int64_t src = (p & 16) ? F + j : j;
+  const uint8_t* s = w + src * K;
+  uint8_t* d = wo + p * K;
+  for (int64_t k = threadIdx.x; k < K; k += kBlock) d[k] = s[k];
+  if (threadIdx.x == 0) {
+    so[p] = scale[src];
+    if (bias && bo) bo[p] = bias[src];
+  }
+}
+
+}  // namespace
+}  // namespace ifx
+
+using namespace ifx;
+
+extern "C" {
+
+int ifx_abi_version(void) { return IFX_ABI_VERSION; }
+
+const char* ifx_status_string(int status) {
+  switch (status) {
+    case IFX_OK: return "ok";
+    case IFX_ERR_INVALID: return "invalid size, stride or flag";
+    case IFX_ERR_ALIGN: return "pointer or stride breaks 16-byte alignment";
+    case IFX_ERR_WORKSPACE: return "workspace missing or too small";
+    case IFX_ERR_UNSUPPORTED: return "shape not supported by any kernel variant";
+    default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
+  }
+}
+
+int ifx_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, void* q,
+                   int64_t ldq, float* scale, void* stream) {
+  if (M < 0 || K < 0 || ldx < K || ldq < K) return IFX_ERR_INVALID;
+  if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec_ok = aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
+  if (x_dtype == IFX_DTYPE_BF16) {
+    SrcBf16 s{static_cast<const uint16_t*>(x), ldx};
+    return dispatch_rows(s, vec_ok && ldx % 8 == 0, M, K, static_cast<uint8_t*>(q), ldq, scale, st);
+  }
+  if (x_dtype == IFX_DTYPE_F32) {
+    SrcF32 s{static_cast<const float*>(x), ldx};
+    return dispatch_rows(s, vec_ok && ldx % 4 == 0, M, K, static_cast<uint8_t*>(q), ldq, scale, st);
+  }
+  return IFX_ERR_INVALID;
+}
+
+size_t ifx_quant_tensor_workspace_size(int64_t count) {
+  if (count <= 0) return 0;
+  return static_cast<size_t>((count + kTensorChunk - 1) / kTensorChunk) * sizeof(uint32_t);
+}
+
+int ifx_quant_tensor_bf16(const void* x, int64_t count, void* q, float* scale, void* partial,
+                          size_t partial_bytes, void* stream) {
+  if (count <= 0 || !x || !q || !scale) return IFX_ERR_INVALID;
+  const int64_t nparts = (count + kTensorChunk - 1) / kTensorChunk;
+  if (nparts > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
+  if (!partial || partial_bytes < ifx_quant_tensor_workspace_size(count)) return IFX_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tensor_amax_partial, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(x), count, static_cast<uint32_t*>(partial));
+  hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(x), count,
+                     static_cast<const uint32_t*>(partial), nparts, static_cast<uint8_t*>(q), scale);
+  return launch_status();
+}
+
+int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void* q, void* stream) {
+  if (count < 0 || (count > 0 && (!x || !q || !scale))) return IFX_ERR_INVALID;
+  if (count == 0) return IFX_OK;
+  const int64_t nparts = (count + kTensorChunk - 1) / kTensorChunk;
+  if (nparts > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
+  hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), count,
+                     static_cast<const uint32_t*>(nullptr), nparts, static_cast<uint8_t*>(q),
+                     const_cast<float*>(scale));
+  return launch_status();
+}
+
+int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row,
+                  const float* col, const float* bias, int gelu, void* q, int64_t ldq,
+                  float* scale, void* stream) {
+  if (M < 0 || K < 0 || ldx < K || ldq < K) return IFX_ERR_INVALID;
+  if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
+  SrcAffine s{static_cast<const uint16_t*>(x), ldx, row, col, bias, gelu ? 1 : 0};
+  const bool vec_ok = aligned16(x) && ldx % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
+  return dispatch_rows(s, vec_ok, M, K, static_cast<uint8_t*>(q), ldq, scale,
+                       static_cast<hipStream_t>(stream));
+}
+
+int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row,
+                        const float* col, int act, void* q, int64_t ldq, float* scale, void* stream) {
+  if (M < 0 || F < 0 || ldgu < 2 * F || ldq < F) return IFX_ERR_INVALID;
+  if (act != IFX_ACT_GELU_TANH && act != IFX_ACT_SILU) return IFX_ERR_INVALID;
+  if (M > 0 && (!gu || !q || !scale)) return IFX_ERR_INVALID;
+  SrcGated s{static_cast<const uint16_t*>(gu), ldgu, F, row, col, act};
+  const bool vec_ok = aligned16(gu) && ldgu % 8 == 0 && F % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
+  return dispatch_rows(s, vec_ok, M, F, static_cast<uint8_t*>(q), ldq, scale,
+                       static_cast<hipStream_t>(stream));
+}
+
+int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const float* row,
+                     const float* col, const float* bias, void* y, int y_dtype, int64_t ldy,
+                     void* stream) {
+  if (M < 0 || D < 0 || ldx < D || ldy < D || M > 65535) return IFX_ERR_INVALID;
+  if (y_dtype != IFX_DTYPE_BF16 && y_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
+  if (M == 0 || D == 0) return IFX_OK;
+  if (!x || !y) return IFX_ERR_INVALID;
+  const dim3 grid(static_cast<unsigned>((D + kBlock - 1) / kBlock), static_cast<unsigned>(M));
+  hipLaunchKernelGGL(dequant_rows_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x), ldx, M, D, row, col, bias, y,
+                     y_dtype == IFX_DTYPE_F32 ? 1 : 0, ldy);
+  return launch_status();
+}
+
+int ifx_fp8_pack_glu(const void* w, const float* scale, const float* bias, int64_t F, int64_t K,
+                     void* w_out, float* scale_out, float* bias_out, void* stream) {
+  if (F <= 0 || K <= 0 || F % 16 != 0 || !w || !scale || !w_out || !scale_out) return IFX_ERR_INVALID;
+  if (2 * F > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
+  hipLaunchKernelGGL(pack_glu_kernel, dim3(static_cast<unsigned>(2 * F)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w), scale, bias, F,
+                     K, static_cast<uint8_t*>(w_out), scale_out, bias_out);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,349 @@
+"""Seeded synthetic workloads for the five benchmark configurations of the FP8
+projection path (shapes from the reference engines' FP8 call sites:
+instinctflash/engines/pi05/engine.py:211-214,241, engines/groot_n17/engine.py:184-188,
+engines/vla4/engine.py:123-137, engines/wan_va/engine.py:214-245).
+
+Inputs are generated on the CPU with torch.Generator (fixed order: activations,
+weights, bias, residual, gate) and copied to the device once; weights are
+quantized once with this package's quantize_weight. A workload's ``step()`` runs
+the whole path for one batch: per-token quantization of every projection input,
+each FP8 GEMM with its fused epilogue, and the re-quantization of GLU/GELU
+outputs that feed a down projection.
+
+For M <= 64 the weights rotate through a pool larger than the MI355X's 256 MB
+Infinity Cache, so consecutive steps stream weights from HBM, as an engine with
+many layers does.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .kernels import fp8 as F
+
+INFINITY_CACHE_BYTES = 256 << 20
+
+
+@dataclass
+class Gemm:
+    """One projection: shapes, fused epilogue and its algorithmic traffic."""
+    name: str
+    M: int
+    N: int          # weight rows (2F for GLU)
+    K: int
+    act: str | None = None
+    bias: bool = False
+    residual: bool = False
+    gate: bool = False
+
+    @property
+    def n_out(self) -> int:
+        return self.N // 2 if self.act in ("geglu", "swiglu") else self.N
+
+    @property
+    def flops(self) -> int:
+        return 2 * self.M * self.N * self.K
+
+    @property
+    def bytes(self) -> int:
+        # A + W + sa + sw + bias(f32) + gate(bf16) + residual(bf16) + out(bf16)
+        b = self.M * self.K + self.N * self.K + 4 * self.M + 4 * self.N
+        b += 4 * self.N if self.bias else 0
+        b += 2 * self.n_out if self.gate else 0
+        b += 2 * self.M * self.n_out if self.residual else 0
+        return b + 2 * self.M * self.n_out
+
+
+def quant_bytes(M: int, K: int) -> int:
+    """bf16 in + e4m3 out + f32 scale."""
+    return 3 * M * K + 4 * M
+
+
+@dataclass
+class Workload:
+    key: str
+    title: str
+    bound: str                      # "hbm" or "mfma"
+    gemms: list
+    quants: list                    # (M, K) of every quantizer pass per step
+    steps_per_unit: int = 1         # C2: 4 flow-matching steps per timed unit
+    pool: int = 1                   # rotating weight sets
+    dominant: str = ""              # name of the kernel the roofline line reports
+    tensors: dict = field(default_factory=dict)
+    _i: int = 0
+
+    @property
+    def flops(self) -> int:
+        return self.steps_per_unit * sum(g.flops for g in self.gemms)
+
+    @property
+    def gemm_bytes(self) -> int:
+        return self.steps_per_unit * sum(g.bytes for g in self.gemms)
+
+    @property
+    def quant_bytes(self) -> int:
+        return self.steps_per_unit * sum(quant_bytes(m, k) for m, k in self.quants)
+
+    @property
+    def bytes(self) -> int:
+        return self.gemm_bytes + self.quant_bytes
+
+    def step(self):
+        self._run(self._i % self.pool)
+        self._i += 1
+
+    def _run(self, p: int):
+        raise NotImplementedError
+
+    def dominant_call(self, p: int):
+        """Launch only the dominant kernel (its inputs prepared by an earlier step)."""
+        raise NotImplementedError
+
+    @property
+    def dominant_gemm(self) -> Gemm:
+        return next(g for g in self.gemms if g.name == self.dominant)
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _act(g, M, K, outlier_frac=0.0, outlier_std=20.0):
+    x = torch.randn((M, K), generator=g)
+    if outlier_frac:
+        mask = torch.rand((M, K), generator=g) < outlier_frac
+        x = torch.where(mask, torch.randn((M, K), generator=g) * outlier_std, x)
+    return x
+
+
+def _weights(g, N, K, dev, bias=False, glu=False):
+    w = torch.randn((N, K), generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.01 if bias else None
+    fw = F.quantize_weight(w, b, device=dev)
+    return F.pack_glu(fw) if glu else fw
+
+
+def _pool_size(bytes_per_set: int) -> int:
+    return max(1, -(-(INFINITY_CACHE_BYTES + (32 << 20)) // bytes_per_set))
+
+
+class _Buffers:
+    def __init__(self, dev):
+        self.dev = dev
+
+    def q(self, M, K):
+        return (torch.empty((M, K), dtype=F.E4M3, device=self.dev), torch.empty(M, dtype=torch.float32, device=self.dev))
+
+
+# ---------------------------------------------------------------------------
+# C1: pi05 action-expert MLP up-projection, M=50 (HBM-bound)
+# ---------------------------------------------------------------------------
+
+class C1(Workload):
+    def __init__(self, dev, seed=0, pool=None):
+        M, K, N = 50, 1024, 4096
+        super().__init__("C1", "pi05 expert up-proj 50x1024->4096 +bias", "hbm",
+                         [Gemm("up", M, N, K, bias=True)], [(M, K)], dominant="up")
+        g = _gen(seed)
+        x = _act(g, M, K, outlier_frac=0.01)
+        self.pool = pool or _pool_size(N * K)
+        ws = [_weights(g, N, K, dev, bias=True)]
+        # Rotated copies of the same quantized weight: identical numerics, distinct HBM lines.
+        ws += [F.Fp8Weight(ws[0].w.clone(), ws[0].scale.clone(), ws[0].bias.clone()) for _ in range(self.pool - 1)]
+        b = _Buffers(dev)
+        self.tensors = dict(x=x.to(torch.bfloat16).to(dev), w=ws, qa=b.q(M, K),
+                            out=torch.empty((M, N), dtype=torch.bfloat16, device=dev))
+
+    def _run(self, p):
+        t = self.tensors
+        qa, sa = t["qa"]
+        F.quant_rows(t["x"], qa, sa)
+        F.linear(qa, sa, t["w"][p], out=t["out"])
+
+    def dominant_call(self, p):
+        t = self.tensors
+        F.linear(*t["qa"], t["w"][p % self.pool], out=t["out"])
+
+
+# ---------------------------------------------------------------------------
+# C2: GR00T-style DiT action head, M=16, up(GELU) + down(+residual) x 4 steps
+# ---------------------------------------------------------------------------
+
+class C2(Workload):
+    def __init__(self, dev, seed=0, pool=None):
+        M, D, FF = 16, 1536, 6144
+        super().__init__("C2", "GR00T DiT M=16: 1536->6144 GELU, 6144->1536 +res, x4 steps", "hbm",
+                         [Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True)],
+                         [(M, D), (M, FF)], steps_per_unit=4, dominant="up")
+        g = _gen(seed)
+        xs = [_act(g, M, D) for _ in range(4)]  # fresh x per flow-matching step
+        w1 = _weights(g, FF, D, dev)
+        w2 = _weights(g, D, FF, dev)
+        res = torch.randn((M, D), generator=g).to(torch.bfloat16)
+        self.pool = pool or _pool_size(2 * FF * D)
+        w1s = [w1] + [F.Fp8Weight(w1.w.clone(), w1.scale.clone()) for _ in range(self.pool - 1)]
+        w2s = [w2] + [F.Fp8Weight(w2.w.clone(), w2.scale.clone()) for _ in range(self.pool - 1)]
+        b = _Buffers(dev)
+        self.tensors = dict(xs=[x.to(torch.bfloat16).to(dev) for x in xs], w1=w1s, w2=w2s, res=res.to(dev),
+                            q1=b.q(M, D), q2=b.q(M, FF), h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
+                            out=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
+
+    def _run(self, p):
+        t = self.tensors
+        q1, s1 = t["q1"]
+        q2, s2 = t["q2"]
+        for s in range(4):
+            # one weight set per (step, flow step): a deep DiT streams each layer's weights
+            i = (p * 4 + s) % self.pool
+            F.quant_rows(t["xs"][s], q1, s1)
+            F.linear(q1, s1, t["w1"][i], out=t["h"], act="gelu_tanh")
+            F.quant_rows(t["h"], q2, s2)
+            F.linear(q2, s2, t["w2"][i], out=t["out"], residual=t["res"])
+
+    def dominant_call(self, p):
+        t = self.tensors
+        F.linear(*t["q1"], t["w1"][p % self.pool], out=t["h"], act="gelu_tanh")
+
+
+# ---------------------------------------------------------------------------
+# C3: pi05 PaliGemma prefix MLP, M=816, GeGLU + down(+residual)
+# ---------------------------------------------------------------------------
+
+class C3(Workload):
+    def __init__(self, dev, seed=0):
+        M, D, FF = 816, 2048, 16384
+        super().__init__("C3", "pi05 prefix MLP M=816: 2048->2x16384 GeGLU, 16384->2048 +res", "mfma",
+                         [Gemm("gate_up", M, 2 * FF, D, act="geglu"), Gemm("down", M, D, FF, residual=True)],
+                         [(M, D), (M, FF)], dominant="gate_up")
+        g = _gen(seed)
+        x = torch.randn((M, D), generator=g)
+        x = x / x.pow(2).mean(dim=1, keepdim=True).sqrt()  # unit-RMS rows (post-RMSNorm)
+        wgu = _weights(g, 2 * FF, D, dev, glu=True)
+        wd = _weights(g, D, FF, dev)
+        res = torch.randn((M, D), generator=g).to(torch.bfloat16)
+        b = _Buffers(dev)
+        self.tensors = dict(x=x.to(torch.bfloat16).to(dev), wgu=wgu, wd=wd, res=res.to(dev), q1=b.q(M, D),
+                            q2=b.q(M, FF), h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
+                            out=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
+
+    def _run(self, p):
+        t = self.tensors
+        q1, s1 = t["q1"]
+        q2, s2 = t["q2"]
+        F.quant_rows(t["x"], q1, s1)
+        F.linear(q1, s1, t["wgu"], out=t["h"], act="geglu")
+        F.quant_rows(t["h"], q2, s2)
+        F.linear(q2, s2, t["wd"], out=t["out"], residual=t["res"])
+
+    def dominant_call(self, p):
+        t = self.tensors
+        F.linear(*t["q1"], t["wgu"], out=t["h"], act="geglu")
+
+
+# ---------------------------------------------------------------------------
+# C4: Qwen2.5-style decoder layer projections (LingBot-VLA-4B), M=1024
+# ---------------------------------------------------------------------------
+
+def _channel_outliers(g, M, K, n=8, factor=30.0):
+    x = torch.randn((M, K), generator=g)
+    ch = torch.randperm(K, generator=g)[:n]
+    x[:, ch] *= factor
+    return x
+
+
+class C4(Workload):
+    def __init__(self, dev, seed=0):
+        M, D, FF = 1024, 2048, 11008
+        qkv_n = 2048 + 256 + 256
+        super().__init__("C4", "VLA4 layer M=1024: qkv(+bias), o(+res), gate|up SwiGLU, down(+res)", "mfma",
+                         [Gemm("qkv", M, qkv_n, D, bias=True), Gemm("o", M, D, D, residual=True),
+                          Gemm("gate_up", M, 2 * FF, D, act="swiglu"), Gemm("down", M, D, FF, residual=True)],
+                         [(M, D), (M, D), (M, D), (M, FF)], dominant="gate_up")
+        g = _gen(seed)
+        x_attn_in = _channel_outliers(g, M, D)
+        x_o_in = _channel_outliers(g, M, D)
+        x_mlp_in = _channel_outliers(g, M, D)
+        wqkv = _weights(g, qkv_n, D, dev, bias=True)
+        wo = _weights(g, D, D, dev)
+        wgu = _weights(g, 2 * FF, D, dev, glu=True)
+        wd = _weights(g, D, FF, dev)
+        res = torch.randn((M, D), generator=g).to(torch.bfloat16)
+        b = _Buffers(dev)
+        bf = lambda t: t.to(torch.bfloat16).to(dev)  # noqa: E731
+        self.tensors = dict(xa=bf(x_attn_in), xo=bf(x_o_in), xm=bf(x_mlp_in), wqkv=wqkv, wo=wo, wgu=wgu, wd=wd,
+                            res=res.to(dev), q=b.q(M, D), qh=b.q(M, FF),
+                            qkv=torch.empty((M, qkv_n), dtype=torch.bfloat16, device=dev),
+                            h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
+                            r1=torch.empty((M, D), dtype=torch.bfloat16, device=dev),
+                            r2=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
+
+    def _run(self, p):
+        t = self.tensors
+        q, s = t["q"]
+        qh, sh = t["qh"]
+        F.quant_rows(t["xa"], q, s)
+        F.linear(q, s, t["wqkv"], out=t["qkv"])
+        F.quant_rows(t["xo"], q, s)
+        F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"])
+        F.quant_rows(t["xm"], q, s)
+        F.linear(q, s, t["wgu"], out=t["h"], act="swiglu")
+        F.quant_rows(t["h"], qh, sh)
+        F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"])
+
+    def dominant_call(self, p):
+        t = self.tensors
+        F.linear(*t["q"], t["wgu"], out=t["h"], act="swiglu")
+
+
+# ---------------------------------------------------------------------------
+# C5: Wan-style video DiT block projections (LingBot-VA), M=8192
+# ---------------------------------------------------------------------------
+
+class C5(Workload):
+    def __init__(self, dev, seed=0):
+        M, D, FF = 8192, 3072, 14336
+        super().__init__("C5", "Wan DiT block M=8192: qkv, o(gated res), up GELU, down(gated res)", "mfma",
+                         [Gemm("qkv", M, 3 * D, D), Gemm("o", M, D, D, residual=True, gate=True),
+                          Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True, gate=True)],
+                         [(M, D), (M, D), (M, D), (M, FF)], dominant="up")
+        g = _gen(seed)
+        mod = torch.rand(D, generator=g) + 0.5  # adaLN modulation scale U(0.5, 1.5) per channel
+        xa = torch.randn((M, D), generator=g) * mod
+        xo = torch.randn((M, D), generator=g) * mod
+        xm = torch.randn((M, D), generator=g) * mod
+        wqkv = _weights(g, 3 * D, D, dev)
+        wo = _weights(g, D, D, dev)
+        wu = _weights(g, FF, D, dev)
+        wd = _weights(g, D, FF, dev)
+        res = torch.randn((M, D), generator=g).to(torch.bfloat16)
+        gate_o = torch.rand(D, generator=g).to(torch.bfloat16)
+        gate_f = torch.rand(D, generator=g).to(torch.bfloat16)
+        b = _Buffers(dev)
+        bf = lambda t: t.to(torch.bfloat16).to(dev)  # noqa: E731
+        self.tensors = dict(xa=bf(xa), xo=bf(xo), xm=bf(xm), wqkv=wqkv, wo=wo, wu=wu, wd=wd, res=res.to(dev),
+                            gate_o=gate_o.to(dev), gate_f=gate_f.to(dev), q=b.q(M, D), qh=b.q(M, FF),
+                            qkv=torch.empty((M, 3 * D), dtype=torch.bfloat16, device=dev),
+                            h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
+                            r1=torch.empty((M, D), dtype=torch.bfloat16, device=dev),
+                            r2=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
+
+    def _run(self, p):
+        t = self.tensors
+        q, s = t["q"]
+        qh, sh = t["qh"]
+        F.quant_rows(t["xa"], q, s)
+        F.linear(q, s, t["wqkv"], out=t["qkv"])
+        F.quant_rows(t["xo"], q, s)
+        F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"], gate=t["gate_o"])
+        F.quant_rows(t["xm"], q, s)
+        F.linear(q, s, t["wu"], out=t["h"], act="gelu_tanh")
+        F.quant_rows(t["h"], qh, sh)
+        F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"], gate=t["gate_f"])
+
+    def dominant_call(self, p):
+        t = self.tensors
+        F.linear(*t["q"], t["wu"], out=t["h"], act="gelu_tanh")
+
+
+CONFIGS = {"C1": C1, "C2": C2, "C3": C3, "C4": C4, "C5": C5}

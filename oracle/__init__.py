@@ -1,0 +1,196 @@
+"""CPU oracle of the FP8 projection path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package, and only as the checker (or, for bench.py, as the timed CPU
+baseline). The product (instinctflash_amd/) never imports it.
+
+Parts
+  * quantizer: plain C restatement (ifx_oracle.c, built by the Makefile here)
+    of instinctflash/kernels/fp8.py:30-37 with the device scale arithmetic of
+    instinctflash/runtime/fp8_pack.py:63-91. Pinned in tests/test_oracle.py by
+    the reference's known-answer scale (tests/test_sm89_fp8.py:48-56), by
+    byte-equality with torch's own CPU E4M3 cast over every finite bf16 pattern
+    and the reference's fixed midpoint scales (scripts/qualify_sm89_fp8.py:61),
+    by NaN/inf propagation, and by a brute-force nearest-value search.
+  * e4m3_decode: the OCP E4M3FN value table, pinned against torch's decoder.
+  * ref_linear: dequantize-then-fp32-matmul (benchmarks/native/fp8_probe.py:36)
+    followed by the epilogue math of kernels/norm.py:45-58,135-144,161-175 and
+    kernels/activation.py:26-40. Pinned by fp64 brute force, closed forms and
+    torch's independent GELU/SiLU implementations.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libifx_oracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB))
+        P, I64 = ctypes.c_void_p, ctypes.c_int64
+        lib.oracle_e4m3.restype = ctypes.c_uint8
+        lib.oracle_e4m3.argtypes = [ctypes.c_float]
+        for name in ("oracle_quant_rows_f32", "oracle_quant_rows_bf16"):
+            getattr(lib, name).restype = None
+            getattr(lib, name).argtypes = [P, I64, I64, I64, P, I64, P]
+        lib.oracle_pack_bf16.restype = None
+        lib.oracle_pack_bf16.argtypes = [P, I64, ctypes.c_float, P]
+        lib.oracle_quant_tensor_bf16.restype = None
+        lib.oracle_quant_tensor_bf16.argtypes = [P, I64, P, P]
+        _lib = lib
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# quantizer
+# ---------------------------------------------------------------------------
+
+def quant_rows(x: np.ndarray):
+    """x: uint16 (bf16 bit patterns) or float32 [M, K] -> (q uint8 [M, K], scale float32 [M])."""
+    x = np.ascontiguousarray(x)
+    M, K = x.shape
+    q = np.empty((M, K), np.uint8)
+    s = np.empty((M,), np.float32)
+    if x.dtype == np.uint16:
+        load().oracle_quant_rows_bf16(_p(x), K, M, K, _p(q), K, _p(s))
+    elif x.dtype == np.float32:
+        load().oracle_quant_rows_f32(_p(x), K, M, K, _p(q), K, _p(s))
+    else:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    return q, s
+
+
+def pack_fixed(x_bf16: np.ndarray, scale: float) -> np.ndarray:
+    x = np.ascontiguousarray(x_bf16.reshape(-1))
+    q = np.empty(x.shape, np.uint8)
+    load().oracle_pack_bf16(_p(x), x.size, float(scale), _p(q))
+    return q.reshape(x_bf16.shape)
+
+
+def quant_tensor(x_bf16: np.ndarray):
+    x = np.ascontiguousarray(x_bf16.reshape(-1))
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty((1,), np.float32)
+    load().oracle_quant_tensor_bf16(_p(x), x.size, _p(q), _p(s))
+    return q.reshape(x_bf16.shape), s
+
+
+def e4m3(values) -> np.ndarray:
+    lib = load()
+    v = np.asarray(values, np.float32).reshape(-1)
+    return np.array([lib.oracle_e4m3(float(f)) for f in v], np.uint8)
+
+
+# ---------------------------------------------------------------------------
+# value tables and conversions
+# ---------------------------------------------------------------------------
+
+def _decode_table() -> np.ndarray:
+    t = np.empty(256, np.float32)
+    for c in range(256):
+        sign = -1.0 if c & 0x80 else 1.0
+        e, m = (c >> 3) & 15, c & 7
+        if e == 15 and m == 7:
+            t[c] = np.nan
+        elif e == 0:
+            t[c] = sign * m * 2.0 ** -9
+        else:
+            t[c] = sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+E4M3_VALUES = _decode_table()
+
+
+def e4m3_decode(q: np.ndarray) -> np.ndarray:
+    return E4M3_VALUES[np.asarray(q, np.uint8)]
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even FP32 -> bf16 bit patterns (NaN kept quiet)."""
+    u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(f, np.float32))
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+# ---------------------------------------------------------------------------
+# GEMM + epilogue
+# ---------------------------------------------------------------------------
+
+def gelu_tanh(x):
+    x = np.asarray(x, np.float32)
+    return (0.5 * x * (1.0 + np.tanh(np.float32(0.7978845608028654) * (x + np.float32(0.044715) * x ** 3)))).astype(np.float32)
+
+
+def silu(x):
+    x = np.asarray(x, np.float32)
+    return (x / (1.0 + np.exp(-x))).astype(np.float32)
+
+
+def ref_linear(qa, sa, qw, sw, bias=None, act=None, residual=None, gate=None, acc_dtype=np.float32):
+    """Dequantize-then-matmul reference (benchmarks/native/fp8_probe.py:36).
+
+    qa uint8 [M,K] / sa [M] (None = 1); qw uint8 [N,K] / sw [N] (None = 1), gate|up
+    weights in the reference layout (rows [0,F) gate, [F,2F) up). act in
+    {None, 'gelu_tanh', 'geglu', 'swiglu'}. gate/residual are float arrays
+    (bf16 values widened). Returns float32 [M, N_out] before output rounding.
+    """
+    a = e4m3_decode(qa).astype(acc_dtype)
+    w = e4m3_decode(qw).astype(acc_dtype)
+    if sa is not None:
+        a = a * np.asarray(sa, acc_dtype)[:, None]
+    if sw is not None:
+        w = w * np.asarray(sw, acc_dtype)[:, None]
+    y = (a @ w.T).astype(np.float32)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float32)[None, :]
+    if act == "gelu_tanh":
+        y = gelu_tanh(y)
+    elif act in ("geglu", "swiglu"):
+        F = y.shape[1] // 2
+        g, u = y[:, :F], y[:, F:]
+        y = (gelu_tanh(g) if act == "geglu" else silu(g)) * u
+    elif act is not None:
+        raise ValueError(act)
+    if gate is not None:
+        y = y * np.asarray(gate, np.float32)[None, :]
+    if residual is not None:
+        y = np.asarray(residual, np.float32) + y
+    return y.astype(np.float32)
+
+
+def parity_stats(out: np.ndarray, ref: np.ndarray):
+    """(max|d| / rms(ref), cosine) -- the GEMM acceptance metrics."""
+    o = np.asarray(out, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    rms = float(np.sqrt(np.mean(r * r))) or 1.0
+    d = float(np.max(np.abs(o - r))) if o.size else 0.0
+    den = float(np.linalg.norm(o) * np.linalg.norm(r))
+    cos = float(np.dot(o, r) / den) if den else 1.0
+    return d / rms, cos

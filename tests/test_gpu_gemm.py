@@ -1,0 +1,231 @@
+"""GPU parity of the FP8 GEMM + fused epilogue against the dequantize-then-fp32-matmul
+oracle (benchmarks/native/fp8_probe.py:36 in the reference).
+
+Acceptance: max|d| <= 2e-2 * rms(ref) and cosine >= 0.9999,
+for every epilogue and both kernel families (skinny M <= 64, LDS-tiled M > 64),
+including ragged M/N/K tails, strided operands, in-place residual and determinism.
+
+The tolerance gates the kernel's arithmetic through its fp32-output mode (same
+kernel, same code path; only the final store differs). The bf16 output is then
+required to be bit-identical to round-to-nearest-even of that fp32 output. The
+split matters for heavy-tailed outputs (GeGLU/SwiGLU, max/rms ~ 25): there bf16
+rounding alone moves the largest values by up to 2^-8 * 25 rms = 0.1 rms,
+which no bf16 result could keep under 2e-2 rms.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAXD = 2e-2   # max|d| / rms(ref)
+TOL_COS = 0.9999
+
+
+def _q(t):
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def _f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _make(gpu, M, N, K, seed, wscale=0.02, bias=False):
+    from instinctflash_amd.kernels import quant_rows, quantize_weight
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), generator=g) * wscale
+    b = torch.randn(N, generator=g) * 0.01 if bias else None
+    fw = quantize_weight(w, b, device=gpu)
+    qa, sa = quant_rows(x.to(gpu))
+    return qa, sa, fw, g
+
+
+def _assert_close(out, ref, what=""):
+    from oracle import parity_stats
+    d, cos = parity_stats(out, ref)
+    assert np.isfinite(out).all(), f"{what}: non-finite output"
+    assert d <= TOL_MAXD and cos >= TOL_COS, f"{what}: max|d|/rms={d:.3e} cos={cos:.6f}"
+
+
+def _ref(oracle_mod, qa, sa, fw, **kw):
+    return oracle_mod.ref_linear(_q(qa), _f(sa), _q(fw.w), _f(fw.scale),
+                                 bias=None if fw.bias is None else _f(fw.bias), **kw)
+
+
+def _check(gpu, oracle_mod, qa, sa, fw, what, ref_w=None, act=None, residual=None, gate=None):
+    """fp32-output arithmetic within tolerance + bf16 output == RNE(fp32 output)."""
+    from instinctflash_amd.kernels import linear
+    r = None if residual is None else residual.to(gpu)
+    gt = None if gate is None else gate.to(gpu)
+    o32 = linear(qa, sa, fw, act=act, residual=r, gate=gt, out_dtype=torch.float32)
+    o16 = linear(qa, sa, fw, act=act, residual=r, gate=gt, out_dtype=torch.bfloat16)
+    ref = _ref(oracle_mod, qa, sa, ref_w or fw, act=act,
+               residual=None if residual is None else residual.float().numpy(),
+               gate=None if gate is None else gate.float().numpy())
+    _assert_close(_f(o32), ref, what)
+    assert torch.equal(o16.view(torch.int16), o32.to(torch.bfloat16).view(torch.int16)), f"{what}: bf16 store"
+    return o32, o16
+
+
+SHAPES = [
+    (1, 16, 128), (16, 6144, 1536), (16, 1536, 6144), (50, 4096, 1024), (64, 256, 2048),
+    (33, 48, 176), (65, 256, 1024), (130, 272, 384), (256, 512, 1024), (300, 1040, 1040),
+    (816, 2048, 256), (1024, 2560, 2048),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_linear_plain(gpu, oracle_mod, M, N, K):
+    qa, sa, fw, _ = _make(gpu, M, N, K, seed=M * 7 + N + K)
+    _check(gpu, oracle_mod, qa, sa, fw, f"{M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(50, 4096, 1024), (16, 512, 256), (200, 2560, 2048)])
+def test_raw_gemm_unit_scales(gpu, oracle_mod, M, N, K):
+    # reference kernels/fp8.py:50-53: raw accumulator in bf16, unit scales.
+    from instinctflash_amd.kernels import gemm
+    qa, sa, fw, _ = _make(gpu, M, N, K, seed=3)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    gemm(qa, fw, out)
+    ref = oracle_mod.ref_linear(_q(qa), None, _q(fw.w), None)
+    _assert_close(_f(out), ref, "raw")
+    # Error budget against the exact sum: bf16 rounding of the result (2^-8
+    # relative) plus the matrix core's accumulation error. One FP8 MFMA adds its
+    # 128 products with an error of at most ~2^-16 of their absolute sum
+    # (measured on gfx950; fp32 adds would give 2^-24), so allow 2^-14.
+    A = oracle_mod.e4m3_decode(_q(qa)).astype(np.float64)
+    W = oracle_mod.e4m3_decode(_q(fw.w)).astype(np.float64)
+    exact, absum = A @ W.T, np.abs(A) @ np.abs(W).T
+    assert np.all(np.abs(_f(out) - exact) <= 2.0 ** -8 * np.abs(exact) + 2.0 ** -14 * absum)
+
+
+@pytest.mark.parametrize("M", [16, 50, 300])
+def test_bias_gelu(gpu, oracle_mod, M):
+    qa, sa, fw, _ = _make(gpu, M, 6144, 1536, seed=M, bias=True)
+    _check(gpu, oracle_mod, qa, sa, fw, "gelu", act="gelu_tanh")
+
+
+@pytest.mark.parametrize("M,act", [(16, "geglu"), (50, "swiglu"), (816, "geglu"), (200, "swiglu")])
+def test_glu(gpu, oracle_mod, M, act):
+    from instinctflash_amd.kernels import pack_glu
+    F, K = 1024, 2048
+    qa, sa, fw, _ = _make(gpu, M, 2 * F, K, seed=M + 1, bias=True)
+    packed = pack_glu(fw)
+    o32, _ = _check(gpu, oracle_mod, qa, sa, packed, act, ref_w=fw, act=act)
+    assert o32.shape == (M, F)
+
+
+@pytest.mark.parametrize("M,res_dtype", [(16, torch.bfloat16), (64, torch.float32), (816, torch.bfloat16),
+                                         (200, torch.float32)])
+def test_residual_and_gate(gpu, oracle_mod, M, res_dtype):
+    from instinctflash_amd.kernels import linear
+    N, K = 1536, 6144 if M <= 64 else 2048
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + 2, bias=True)
+    res = torch.randn((M, N), generator=g).to(res_dtype)
+    gate = torch.rand(N, generator=g).to(torch.bfloat16)
+    # plain residual, separate output
+    _check(gpu, oracle_mod, qa, sa, fw, "res", residual=res)
+    o32, o16 = _check(gpu, oracle_mod, qa, sa, fw, "gated", residual=res, gate=gate)
+    # in place (out aliases residual): same bytes as the out-of-place result
+    r = res.to(gpu)
+    linear(qa, sa, fw, out=r, residual=r, gate=gate.to(gpu))
+    expect = o32 if res_dtype == torch.float32 else o16
+    assert torch.equal(r, expect), "in-place residual update differs"
+
+
+def test_fp32_output(gpu, oracle_mod):
+    qa, sa, fw, _ = _make(gpu, 100, 512, 512, seed=8, bias=True)
+    o32, _ = _check(gpu, oracle_mod, qa, sa, fw, "f32 out")
+    assert o32.dtype == torch.float32
+
+
+def test_strided_operands(gpu, oracle_mod):
+    from instinctflash_amd.kernels import linear
+    M, N, K = 96, 256, 512
+    qa, sa, fw, _ = _make(gpu, M, N, K, seed=9)
+    abig = torch.zeros((M, K + 128), dtype=torch.float8_e4m3fn, device=gpu)
+    abig[:, 64:64 + K] = qa
+    obig = torch.zeros((M, N + 64), dtype=torch.bfloat16, device=gpu)
+    out = obig[:, 32:32 + N]
+    linear(abig[:, 64:64 + K], sa, fw, out=out)
+    _assert_close(_f(out), _ref(oracle_mod, qa, sa, fw), "strided")
+    assert not obig[:, :32].any() and not obig[:, 32 + N:].any()
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (50, 4096, 1024), (512, 1024, 2048)])
+def test_deterministic(gpu, M, N, K):
+    from instinctflash_amd.kernels import linear
+    qa, sa, fw, _ = _make(gpu, M, N, K, seed=10)
+    a = linear(qa, sa, fw)
+    for _ in range(3):
+        b = linear(qa, sa, fw)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_edge_rows_untouched(gpu, oracle_mod):
+    # M not a multiple of any tile: rows past M must not be written.
+    from instinctflash_amd.kernels import linear
+    M, N, K = 70, 512, 256
+    qa, sa, fw, _ = _make(gpu, M, N, K, seed=12)
+    obig = torch.full((M + 8, N), 7.0, dtype=torch.bfloat16, device=gpu)
+    linear(qa, sa, fw, out=obig[:M])
+    assert (obig[M:] == 7.0).all()
+
+
+def test_graph_capture_replay(gpu, oracle_mod):
+    from instinctflash_amd.kernels import linear, quant_rows
+    M, N, K = 16, 1536, 6144
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(gpu)
+    from instinctflash_amd.kernels import quantize_weight
+    fw = quantize_weight(torch.randn((N, K), generator=g) * 0.02, device=gpu)
+    qa = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gpu)
+    sa = torch.empty(M, device=gpu)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for _ in range(2):
+            quant_rows(x, qa, sa)
+            linear(qa, sa, fw, out=out)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        quant_rows(x, qa, sa)
+        linear(qa, sa, fw, out=out)
+    for i in range(4):
+        x.copy_(torch.randn((M, K), generator=g).to(torch.bfloat16).to(gpu))
+        graph.replay()
+        torch.cuda.synchronize()
+        q2, s2 = quant_rows(x)
+        eager = linear(q2, s2, fw)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+
+
+def test_contract_errors(gpu):
+    from instinctflash_amd.kernels import linear, pack_glu
+    qa, sa, fw, _ = _make(gpu, 16, 64, 128, seed=14)
+    with pytest.raises(ValueError):
+        linear(qa, sa, fw, act="relu")
+    with pytest.raises(ValueError):
+        linear(qa, sa, fw, act="geglu")  # not packed
+    with pytest.raises(ValueError):
+        linear(qa.float(), sa, fw)
+    with pytest.raises(ValueError):
+        linear(qa[:, :120], sa, fw)
+    p = pack_glu(fw)
+    with pytest.raises(ValueError):
+        linear(qa, sa, p)  # packed weight needs a GLU epilogue
+
+
+def test_workspace_reuse_across_shapes(gpu, oracle_mod):
+    # Regression: split-K calls with different plans share one workspace per
+    # stream; a call must never read another call's partials as its tickets.
+    seq = [(16, 64, 4096), (16, 1536, 6144), (64, 256, 2048), (1, 512, 8192), (16, 1536, 6144), (50, 96, 4096)]
+    for i, (M, N, K) in enumerate(seq):
+        qa, sa, fw, _ = _make(gpu, M, N, K, seed=100 + i)
+        from instinctflash_amd.kernels import linear
+        out = linear(qa, sa, fw, out_dtype=torch.float32)
+        _assert_close(_f(out), _ref(oracle_mod, qa, sa, fw), f"seq {i}: {M}x{N}x{K}")

@@ -1,0 +1,280 @@
+"""GPU parity of the quantizers against the CPU oracle: bit-exact bytes and scales.
+
+Cases follow the reference's own byte-exact tests (tests/test_dynamic_fp8_pack.py:7-38,
+scripts/qualify_sm89_fp8.py:42-80): shapes (40,2048), (256,5120), (1,16); magnitudes 0,
+1e-20, 1e30; every finite bf16 bit pattern; fixed midpoint scales; NaN/inf propagation;
+plus every K of the five benchmark configurations, ragged and strided layouts.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _q(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def _f(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def _nan_eq_bytes(got, exp):
+    """Byte equality; a NaN code only has to be NaN (sign/payload immaterial,
+    scripts/qualify_sm89_fp8.py:71-74)."""
+    g, e = np.asarray(got, np.uint8), np.asarray(exp, np.uint8)
+    nan_e = (e & 0x7F) == 0x7F
+    assert np.array_equal((g & 0x7F) == 0x7F, nan_e)
+    bad = np.nonzero((g != e) & ~nan_e)
+    assert bad[0].size == 0, f"{bad[0].size} differing bytes, first at {tuple(b[0] for b in bad)}"
+
+
+def _check_rows(x: torch.Tensor, oracle_mod):
+    from instinctflash_amd.kernels import quant_rows
+    q, s = quant_rows(x)
+    torch.cuda.synchronize()
+    xo = _bits(x) if x.dtype == torch.bfloat16 else _f(x).astype(np.float32)
+    eq, es = oracle_mod.quant_rows(xo)
+    gs = _f(s)
+    assert np.array_equal(np.isnan(gs), np.isnan(es))
+    assert np.array_equal(gs[~np.isnan(es)].view(np.uint32), es[~np.isnan(es)].view(np.uint32))
+    _nan_eq_bytes(_q(q), eq)
+
+
+def all_finite_bf16():
+    pat = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    return pat[torch.isfinite(pat)].contiguous()  # 65280 values
+
+
+def test_known_answer_scale(gpu):
+    # tests/test_sm89_fp8.py:48-56: amax 0.0361328125 -> scale 0x38A92493.
+    from instinctflash_amd.kernels import quant_rows
+    x = torch.full((1, 16), 0.0361328125, dtype=torch.bfloat16, device=gpu)
+    _, s = quant_rows(x)
+    assert s.cpu().view(torch.int32).item() == 0x38A92493
+
+
+@pytest.mark.parametrize("shape,mag", [((40, 2048), 1.0), ((256, 5120), 1.0), ((1, 16), 0.0),
+                                       ((1, 16), 1e-20), ((1, 16), 1e30)])
+def test_reference_cases(gpu, oracle_mod, shape, mag):
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(shape, generator=g) * mag).to(torch.bfloat16).to(gpu)
+    _check_rows(x, oracle_mod)
+
+
+def test_all_finite_bf16_one_row(gpu, oracle_mod):
+    _check_rows(all_finite_bf16().reshape(1, -1).to(gpu), oracle_mod)
+
+
+def test_all_finite_bf16_many_rows(gpu, oracle_mod):
+    # 255 rows x 256: each row gets its own scale; exercises the register path.
+    x = all_finite_bf16().reshape(255, 256)
+    _check_rows(x.to(gpu), oracle_mod)
+    # and rows shuffled so magnitudes mix within a row
+    perm = torch.randperm(x.numel(), generator=torch.Generator().manual_seed(1))
+    _check_rows(x.reshape(-1)[perm].reshape(255, 256).to(gpu), oracle_mod)
+
+
+@pytest.mark.parametrize("K", [16, 24, 1024, 1536, 2048, 3072, 6144, 11008, 14336, 16384, 20000])
+def test_config_widths(gpu, oracle_mod, K):
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn((37, K), generator=g)
+    mask = torch.rand((37, K), generator=g) < 0.01
+    x = torch.where(mask, torch.randn((37, K), generator=g) * 20, x)
+    _check_rows(x.to(torch.bfloat16).to(gpu), oracle_mod)
+
+
+@pytest.mark.parametrize("K", [1, 13, 1000, 1003])
+def test_ragged_widths(gpu, oracle_mod, K):
+    g = torch.Generator().manual_seed(K)
+    _check_rows(torch.randn((9, K), generator=g).to(torch.bfloat16).to(gpu), oracle_mod)
+
+
+def test_strided_rows(gpu, oracle_mod):
+    from instinctflash_amd.kernels import quant_rows
+    g = torch.Generator().manual_seed(5)
+    big = torch.randn((20, 3072), generator=g).to(torch.bfloat16).to(gpu)
+    x = big[:, 1024:2048]  # row stride 3072
+    qbig = torch.zeros((20, 2048), dtype=torch.float8_e4m3fn, device=gpu)
+    q = qbig[:, 512:1536]
+    s = torch.empty(20, device=gpu)
+    quant_rows(x, q, s)
+    eq, es = oracle_mod.quant_rows(_bits(x))
+    assert np.array_equal(_f(s).view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(_q(q), eq)
+    assert not _q(qbig[:, :512]).any() and not _q(qbig[:, 1536:]).any()
+
+
+def test_empty_rows(gpu):
+    from instinctflash_amd.kernels import quant_rows
+    q, s = quant_rows(torch.empty((0, 64), dtype=torch.bfloat16, device=gpu))
+    assert q.shape == (0, 64) and s.shape == (0,)
+
+
+def test_nonfinite_propagation(gpu, oracle_mod):
+    for bad in (float("nan"), float("inf"), -float("inf")):
+        x = torch.ones((4, 1024), dtype=torch.bfloat16)
+        x[0, 0] = bad
+        x[2, 700] = bad
+        _check_rows(x.to(gpu), oracle_mod)
+
+
+def test_fp32_weight_rows(gpu, oracle_mod):
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn((96, 1536), generator=g) * 0.02
+    w[5] = 0.0
+    w[7, 3] = 1e-30
+    _check_rows(w.to(gpu), oracle_mod)
+    _check_rows(w[:, :1000].contiguous().to(gpu), oracle_mod)
+
+
+def test_quantize_weight_matches_recipe(gpu, oracle_mod):
+    from instinctflash_amd.kernels import quantize_weight
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn((4096, 1024), generator=g) * 0.02
+    b = torch.randn(4096, generator=g)
+    fw = quantize_weight(w, b, device=gpu)
+    eq, es = oracle_mod.quant_rows(w.numpy())
+    assert np.array_equal(_q(fw.w), eq)
+    assert np.array_equal(_f(fw.scale).view(np.uint32), es.view(np.uint32))
+    assert torch.equal(fw.bias.cpu(), b)
+
+
+@pytest.mark.parametrize("scale", [1.0, 1.0 + 2.0 ** -23, 1.0 - 2.0 ** -24, 2.0 ** -16, 1.0 / 448.0])
+def test_fixed_scale_pack_all_patterns(gpu, oracle_mod, scale):
+    # scripts/qualify_sm89_fp8.py:58-67: exact E4M3 midpoints and scales beside one.
+    from instinctflash_amd.kernels import pack_tensor
+    x = all_finite_bf16()
+    s = torch.tensor([scale], dtype=torch.float32)
+    q = pack_tensor(x.to(gpu), s.to(gpu))
+    _nan_eq_bytes(_q(q), oracle_mod.pack_fixed(_bits(x), float(s.item())))
+
+
+@pytest.mark.parametrize("shape,mag", [((40, 2048), 1.0), ((256, 5120), 1.0), ((1, 16), 0.0),
+                                       ((1, 16), 1e-20), ((1, 16), 1e30), ((3, 100003), 1.0)])
+def test_per_tensor_quant(gpu, oracle_mod, shape, mag):
+    from instinctflash_amd.kernels import quantize_tensor
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(shape, generator=g) * mag).to(torch.bfloat16)
+    q, s = quantize_tensor(x.to(gpu))
+    eq, es = oracle_mod.quant_tensor(_bits(x))
+    assert _f(s).view(np.uint32)[0] == es.view(np.uint32)[0]
+    _nan_eq_bytes(_q(q), eq)
+
+
+def test_per_tensor_all_patterns_and_nan(gpu, oracle_mod):
+    from instinctflash_amd.kernels import quantize_tensor
+    x = all_finite_bf16().reshape(1, -1)
+    q, s = quantize_tensor(x.to(gpu))
+    eq, es = oracle_mod.quant_tensor(_bits(x))
+    assert _f(s).view(np.uint32)[0] == es.view(np.uint32)[0]
+    _nan_eq_bytes(_q(q), eq)
+    y = torch.full((40, 2048), float("nan"), dtype=torch.bfloat16, device=gpu)
+    _, s = quantize_tensor(y)
+    assert torch.isnan(s).all()
+
+
+def test_row_quant_affine_bit_exact(gpu, oracle_mod):
+    # reference kernels/norm.py:127-158 without gelu: v = x*row*col + bias in FP32.
+    from instinctflash_amd.kernels import row_quant
+    g = torch.Generator().manual_seed(21)
+    M, D = 50, 2560
+    x = torch.randn((M, D), generator=g).to(torch.bfloat16)
+    row, col, bias = torch.rand(M, generator=g), torch.rand(D, generator=g), torch.randn(D, generator=g)
+    q = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    row_quant(x.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
+    v = (oracle_mod.bf16_to_f32(_bits(x)) * row.numpy()[:, None]).astype(np.float32)
+    v = (v * col.numpy()[None, :]).astype(np.float32) + bias.numpy()[None, :]
+    eq, es = oracle_mod.quant_rows(v.astype(np.float32))
+    assert np.array_equal(_f(s).view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(_q(q), eq)
+
+
+def _deq(q, s):
+    return q.float() * s[:, None]
+
+
+def test_row_quant_gelu(gpu, oracle_mod):
+    from instinctflash_amd.kernels import row_quant
+    g = torch.Generator().manual_seed(22)
+    M, D = 16, 6144
+    x = (torch.randn((M, D), generator=g) * 3).to(torch.bfloat16)
+    q = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    row_quant(x.to(gpu), q, s, gelu=True)
+    h = oracle_mod.gelu_tanh(oracle_mod.bf16_to_f32(_bits(x)))
+    eq, es = oracle_mod.quant_rows(h)
+    # GELU uses the hardware exp2/rcp (a few ulp from numpy's tanh): values may
+    # straddle a rounding boundary, so require scales within 8 ulp, >= 99.9%
+    # identical bytes, and the reference's own envelope
+    # (tests/test_gi_kernels.py:127: |deq - h| / amax < 0.07).
+    assert np.all(np.abs(_f(s).view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
+    assert (_q(q) == eq).mean() > 0.999
+    err = np.abs(_deq(q, s).cpu().numpy() - h) / np.abs(h).max(axis=1, keepdims=True)
+    assert err.max() < 0.07
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_gated_act_quant(gpu, oracle_mod, act):
+    from instinctflash_amd.kernels import gated_act_quant
+    g = torch.Generator().manual_seed(23 + act)
+    M, F = 9, 4096
+    gu = torch.randn((M, 2 * F), generator=g).to(torch.bfloat16)
+    row, col = torch.rand(M, generator=g), torch.rand(2 * F, generator=g)
+    q = torch.empty((M, F), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    gated_act_quant(gu.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu), act=act)
+    x = oracle_mod.bf16_to_f32(_bits(gu)) * row.numpy()[:, None] * col.numpy()[None, :]
+    gg, uu = x[:, :F].astype(np.float32), x[:, F:].astype(np.float32)
+    h = (oracle_mod.gelu_tanh(gg) if act == 0 else oracle_mod.silu(gg)) * uu
+    eq, es = oracle_mod.quant_rows(h.astype(np.float32))
+    assert np.all(np.abs(_f(s).view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
+    assert (_q(q) == eq).mean() > 0.999
+    err = np.abs(_deq(q, s).cpu().numpy() - h) / np.abs(h).max(axis=1, keepdims=True)
+    assert err.max() < 0.07
+
+
+def test_dequant_rows(gpu):
+    from instinctflash_amd.kernels import dequant_rows
+    g = torch.Generator().manual_seed(24)
+    M, D = 50, 4096
+    x = torch.randn((M, D), generator=g).to(torch.bfloat16)
+    row, col, bias = torch.rand(M, generator=g), torch.rand(D, generator=g), torch.randn(D, generator=g)
+    y = torch.empty((M, D), device=gpu)
+    dequant_rows(x.to(gpu), y, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
+    exp = (x.float() * row[:, None]) * col + bias
+    assert torch.equal(y.cpu(), exp)
+    yb = torch.empty((M, D), dtype=torch.bfloat16, device=gpu)
+    dequant_rows(x.to(gpu), yb, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
+    assert torch.equal(yb.cpu(), exp.to(torch.bfloat16))
+
+
+def test_graph_replay_matches_eager(gpu, oracle_mod):
+    # tests/test_dynamic_fp8_pack.py:24-35: captured launches give the eager bytes.
+    from instinctflash_amd.kernels import quant_rows
+    x = torch.randn((40, 2048), device=gpu).to(torch.bfloat16)
+    q = torch.empty((40, 2048), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(40, device=gpu)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            quant_rows(x, q, s)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        quant_rows(x, q, s)
+    for mag in (0.0, 1e-4, 20.0, 1.0):
+        x.copy_(torch.randn_like(x) * mag)
+        graph.replay()
+        torch.cuda.synchronize()
+        qe, se = quant_rows(x)
+        torch.cuda.synchronize()
+        assert torch.equal(s, se)
+        assert torch.equal(q.view(torch.uint8), qe.view(torch.uint8))
