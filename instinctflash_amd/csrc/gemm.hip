@@ -95,26 +95,55 @@ __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, 
   }
 }
 
-// Plain epilogue for one lane's D fragment: rows n..n+3 of W, token m.
-__device__ __forceinline__ void epi_store(const Epi& e, const v4f acc, int64_t n, int64_t m) {
-  if (m >= e.M || n >= e.N) return;
+// First half of the epilogue for one lane's D fragment (weight rows n..n+3,
+// token m): dequantization scales, bias, GELU. Caller guarantees m < M, n < N.
+__device__ __forceinline__ void epi_pre(const Epi& e, const v4f acc, int64_t n, int64_t m, float* y) {
   const float sa = e.sa ? e.sa[m] : 1.0f;
   const float4 sw = load_f4_or(e.sw, n, 1.0f);
   const float4 b = load_f4_or((e.flags & IFX_EPI_BIAS) ? e.bias : nullptr, n, 0.0f);
-  float y[4] = {acc[0] * sa * sw.x + b.x, acc[1] * sa * sw.y + b.y, acc[2] * sa * sw.z + b.z,
-                acc[3] * sa * sw.w + b.w};
+  y[0] = acc[0] * sa * sw.x + b.x;
+  y[1] = acc[1] * sa * sw.y + b.y;
+  y[2] = acc[2] * sa * sw.z + b.z;
+  y[3] = acc[3] * sa * sw.w + b.w;
   if (e.flags & IFX_EPI_GELU_TANH) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) y[r] = gelu_tanh(y[r]);
   }
+}
+
+// Store four finished values at out[m, c..c+3] (bf16, or f32 with IFX_EPI_OUT_F32).
+__device__ __forceinline__ void epi_store4(const Epi& e, int64_t m, int64_t c, const float* y) {
+  if (e.flags & IFX_EPI_OUT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(e.out) + m * e.ldo + c) = make_float4(y[0], y[1], y[2], y[3]);
+  } else {
+    uint2 o;
+    o.x = pack_bf16x2(y[0], y[1]);
+    o.y = pack_bf16x2(y[2], y[3]);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.out) + m * e.ldo + c) = o;
+  }
+}
+
+// residual[m, c..c+3] widened to fp32 (bf16 or f32 residual).
+__device__ __forceinline__ float4 load_res4(const Epi& e, int64_t m, int64_t c) {
+  if (e.flags & IFX_EPI_RES_F32)
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(e.res) + m * e.ldr + c);
+  const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(e.res) + m * e.ldr + c);
+  return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u), __uint_as_float(r.y << 16),
+                     __uint_as_float(r.y & 0xFFFF0000u));
+}
+
+// Plain epilogue for one lane's D fragment: rows n..n+3 of W, token m.
+__device__ __forceinline__ void epi_store(const Epi& e, const v4f acc, int64_t n, int64_t m) {
+  if (m >= e.M || n >= e.N) return;
+  float y[4];
+  epi_pre(e, acc, n, m, y);
   epi_finish4(e, m, n, y);
 }
 
-// GLU epilogue: `ng` is the packed row of the gate fragment, the up fragment is
-// 16 packed rows later; output column = (ng / 32) * 16 + (ng % 16).
-__device__ __forceinline__ void epi_store_glu(const Epi& e, const v4f accg, const v4f accu, int64_t ng,
-                                              int64_t m) {
-  if (m >= e.M || ng >= e.N) return;
+// GLU first half: `ng` is the packed row of the gate fragment, the up fragment
+// is 16 packed rows later. Caller guarantees m < M, ng < N.
+__device__ __forceinline__ void epi_pre_glu(const Epi& e, const v4f accg, const v4f accu, int64_t ng,
+                                            int64_t m, float* y) {
   const float sa = e.sa ? e.sa[m] : 1.0f;
   const float4 swg = load_f4_or(e.sw, ng, 1.0f);
   const float4 swu = load_f4_or(e.sw, ng + 16, 1.0f);
@@ -125,10 +154,17 @@ __device__ __forceinline__ void epi_store_glu(const Epi& e, const v4f accg, cons
                       accg[2] * sa * swg.z + bg.z, accg[3] * sa * swg.w + bg.w};
   const float u[4] = {accu[0] * sa * swu.x + bu.x, accu[1] * sa * swu.y + bu.y,
                       accu[2] * sa * swu.z + bu.z, accu[3] * sa * swu.w + bu.w};
-  float y[4];
   const bool swiglu = (e.flags & IFX_EPI_SWIGLU) != 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r) y[r] = (swiglu ? silu(g[r]) : gelu_tanh(g[r])) * u[r];
+}
+
+// GLU epilogue; output column = (ng / 32) * 16 + (ng % 16).
+__device__ __forceinline__ void epi_store_glu(const Epi& e, const v4f accg, const v4f accu, int64_t ng,
+                                              int64_t m) {
+  if (m >= e.M || ng >= e.N) return;
+  float y[4];
+  epi_pre_glu(e, accg, accu, ng, m, y);
   epi_finish4(e, m, (ng >> 5) * 16 + (ng & 15), y);
 }
 
@@ -169,8 +205,16 @@ struct TileCfg {
   static_assert(2 * kStageBytes <= 160 * 1024, "LDS");
 };
 
-// byte offset of 16-byte chunk `ch` of tile row `row` (XOR swizzle by row).
-__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ (row & 7)) << 4); }
+// Byte offset of 16-byte chunk `ch` of tile row `row` (rows are 128 bytes).
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time from 64 banks (a
+// 256-byte window = two tile rows). A fragment read has 16 lanes on 16
+// consecutive rows with the same logical chunk, so the physical chunk
+// ch ^ f(row), f(row) = (row % 8) ^ ((row / 8) % 2), must put every
+// (row parity, chunk) pair in a different place: f is a bijection on the even
+// and on the odd rows of any 16-row block (and on any 8 consecutive rows,
+// which also keeps a 32-bank, 8-lanes-per-cycle LDS conflict free).
+__device__ __forceinline__ int swz_f(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row, int ch) { return row * kBK + ((ch ^ swz_f(row)) << 4); }
 
 template <int BN, int BM, int WGN, int WGM, bool GLU>
 __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __restrict__ A, int64_t lda,
@@ -286,6 +330,315 @@ __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __re
     for (int i = 0; i < C::kFN; ++i)
 #pragma unroll
       for (int j = 0; j < C::kFM; ++j) epi_store(e, acc[i][j], nb + i * 16, mb + j * 16);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Large-M kernel: direct-to-LDS multi-stage ring, 32x32x64 matrix cores
+// ---------------------------------------------------------------------------
+//
+// Workgroup tile: 256 weight rows x BM tokens, 4 waves in a 2 x 2 grid, wave
+// tile 128 x BM/2, built from v_mfma_f32_32x32x64_f8f6f4 (the 32x32 form keeps
+// the matrix pipe ~97% busy from a single wave per SIMD on gfx950; the 16x16x128
+// form reaches ~75% there). Operand roles as in the other kernels: weights are
+// source 0, so a lane of a 32x32 fragment holds, for q = 0..3, the four
+// consecutive weight rows 8q + 4*(lane/32) + 0..3 of token lane%32.
+//
+// Stage = (256 + BM) rows x KB K-bytes (KB = 64 or 128), STAGES stages in a
+// ring. Global -> LDS copies use gfx950's global_load_lds_dwordx4: one
+// instruction moves 64 lanes x 16 B into a contiguous 1 KB LDS block, lane l
+// landing at byte 16*l; the row swizzle (`Swz`) is therefore applied on the
+// global side, each lane fetching the logical chunk that belongs at its LDS
+// position. K must be a multiple of KB (whole stages, no zero fill).
+//
+// OCC workgroups share a CU (OCC = 2 with 64-byte stages: 3 x 24 KB of LDS and
+// <= 128 VGPRs per wave), so one workgroup's barrier waits, epilogue and store
+// drain overlap the other's matrix-core work.
+//
+// Pipeline: loads run STAGES-1 stages ahead; one barrier per K step.
+//   wait until this wave's loads of stage k landed (vmcnt <= loads still
+//   allowed in flight); s_barrier (stage k visible to all; all waves finished
+//   stage k-1, whose slot is reused next); issue stage k+STAGES-1; MFMAs on k.
+// The barrier is the bare s_barrier: a __syncthreads() fence would also wait
+// for the loads that are meant to stay in flight.
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(1))) void* global_void_ptr;
+
+constexpr int kBigBN = 256;
+
+// LDS layout of a tile with KB-byte rows: 16-byte chunk `ch` of row `row` is
+// stored at chunk position ch ^ f(row). gfx950's LDS serves a ds_read_b128 16
+// lanes at a time from 64 banks (a 256-byte window); a fragment read puts 16
+// lanes on 16 consecutive rows with the same logical chunk, so f must send
+// those 16 reads to 16 different 16-byte bank groups:
+//   KB = 128 (two rows per window): f(r) = (r % 8) ^ ((r / 8) % 2)
+//   KB = 64  (four rows per window): f(r) = (r / 4) % 4
+template <int KB>
+struct Swz {
+  static constexpr int kChunks = KB / 16;
+  static __device__ __forceinline__ int f(int row) {
+    if constexpr (KB == 128) return (row & 7) ^ ((row >> 3) & 1);
+    else return (row >> 2) & 3;
+  }
+  static __device__ __forceinline__ int off(int row, int ch) { return row * KB + ((ch ^ f(row)) << 4); }
+};
+
+// Tile order. The hardware hands workgroup b to XCD b % 8, and each XCD has its
+// own L2. Workgroup b is given logical tile xcd * per_xcd + b / 8, so every XCD
+// walks one contiguous range of logical tiles; logical tiles are ordered in
+// groups of `group_m` token-tile rows, walking the weight tiles inside a group
+// (tile (tm, tn) with tm fastest), so the ~32 tiles an XCD runs at once form a
+// compact block that shares weight and token panels in that XCD's L2.
+struct TileMap {
+  int tiles_m, tiles_n, group_m, per_xcd;
+};
+
+__device__ __forceinline__ bool map_tile(const TileMap& t, int& tm, int& tn) {
+  const int b = blockIdx.x;
+  const int logical = (b & 7) * t.per_xcd + (b >> 3);
+  if (logical >= t.tiles_m * t.tiles_n) return false;
+  const int per_group = t.group_m * t.tiles_n;
+  const int grp = logical / per_group;
+  const int first_m = grp * t.group_m;
+  const int gsize = min(t.tiles_m - first_m, t.group_m);
+  const int r = logical - grp * per_group;
+  tm = first_m + r % gsize;
+  tn = r / gsize;
+  return true;
+}
+
+__host__ inline TileMap make_tile_map(int64_t tiles_m, int64_t tiles_n) {
+  TileMap t;
+  t.tiles_m = static_cast<int>(tiles_m);
+  t.tiles_n = static_cast<int>(tiles_n);
+  t.group_m = static_cast<int>(tiles_m < 4 ? tiles_m : 4);
+  t.per_xcd = static_cast<int>((tiles_m * tiles_n + 7) / 8);
+  return t;
+}
+
+__device__ __forceinline__ v16f mfma32(const v8i& w, const v8i& a, const v16f& c) {
+  // cbsz = blgp = 0: both operands FP8 E4M3 (OCP); no block scales.
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N (0..63).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ v4f quad(const v16f& v, int q) {
+  return v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+}
+
+template <int BM, int KB, int STAGES, int OCC, bool GLU>
+__global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
+                                                     const uint8_t* __restrict__ W, int64_t ldw, int64_t K,
+                                                     TileMap tmap, Epi e) {
+  using S = Swz<KB>;
+  constexpr int kRows = kBigBN + BM;
+  constexpr int kStage = kRows * KB;
+  constexpr int kRowsPerDma = 1024 / KB;           // rows one DMA instruction fills
+  constexpr int kLoads = kRows / kRowsPerDma / 4;  // DMA instructions per wave per stage
+  constexpr int kFN = 4;                           // 32-row weight fragments per wave (128 rows)
+  constexpr int kFM = BM / 64;                     // 32-token fragments per wave
+  constexpr int kHalves = KB / 64;                 // 32x32x64 K steps per stage
+  static_assert(BM % 64 == 0 && kRows % (4 * kRowsPerDma) == 0, "tile");
+  static_assert(KB == 64 || KB == 128, "stage depth");
+  constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
+  constexpr int kEpiBytes = 4 * 32 * kPitch * 4;
+  constexpr int kSmem = STAGES * kStage > kEpiBytes ? STAGES * kStage : kEpiBytes;
+  static_assert(OCC * kSmem <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
+  __shared__ float s_sa[BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wn = wave >> 1;  // weight-row half
+  const int wm = wave & 1;   // token-row half
+
+  int tm, tn;
+  if (!map_tile(tmap, tm, tn)) return;
+  const int64_t n0 = static_cast<int64_t>(tn) * kBigBN;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int nk = static_cast<int>(K / KB);
+
+  // DMA load i of a stage covers rows kRowsPerDma*blk .. +kRowsPerDma-1
+  // (blk = wave*kLoads + i; weight rows first, then token rows). Rows past N/M
+  // are clamped: computed, never stored. Addresses are formed per stage to keep
+  // VGPRs free.
+  const int lrow = lane / S::kChunks;
+  const int lpos = lane % S::kChunks;
+  auto issue = [&](int kt) {
+    uint8_t* buf = smem + (kt % STAGES) * kStage;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int blk = wave * kLoads + i;
+      const int row = blk * kRowsPerDma + lrow;
+      const int64_t k0 = static_cast<int64_t>(kt) * KB + ((lpos ^ S::f(row)) << 4);
+      const uint8_t* p;
+      if (blk * kRowsPerDma < kBigBN) {  // wave-uniform
+        p = W + min(n0 + row, e.N - 1) * ldw + k0;
+      } else {
+        p = A + min(m0 + (row - kBigBN), e.M - 1) * lda + k0;
+      }
+      __builtin_amdgcn_global_load_lds((global_void_ptr)p, (lds_void_ptr)(buf + blk * 1024), 16, 0, 0);
+    }
+  };
+
+  v16f acc[kFN][kFM];
+#pragma unroll
+  for (int i = 0; i < kFN; ++i)
+#pragma unroll
+    for (int j = 0; j < kFM; ++j) acc[i][j] = v16f{};
+
+  // 32x32x64 fragment of K step h of the stage: lane l supplies row l%32 and the
+  // K bytes [64h + 32*(l/32), +32) = chunks 4h + 2*(l/32) + {0,1}.
+  const int frow = lane & 31;
+  const int fhalf = lane >> 5;
+  auto compute = [&](const uint8_t* base) {
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) {
+      const int c0 = 4 * h + 2 * fhalf;
+      v8i af[kFM];
+#pragma unroll
+      for (int j = 0; j < kFM; ++j) {
+        const int row = kBigBN + wm * (BM / 2) + j * 32 + frow;
+        af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
+      }
+#pragma unroll
+      for (int i = 0; i < kFN; ++i) {
+        const int row = wn * 128 + i * 32 + frow;
+        const v8i wf = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
+#pragma unroll
+        for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wf, af[j], acc[i][j]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // Loads of stages kt+1 .. kt+STAGES-2 may stay in flight.
+    if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#ifndef IFX_DBG_NO_DMA
+    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+#endif
+#ifndef IFX_DBG_NO_MFMA
+    compute(smem + (kt % STAGES) * kStage);
+#endif
+  }
+
+#ifdef IFX_DBG_NO_EPI
+  {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kFN; ++i)
+#pragma unroll
+      for (int j = 0; j < kFM; ++j) t += acc[i][j][0] + acc[i][j][7] + acc[i][j][15];
+    if (t == 1234.5f) static_cast<float*>(e.out)[tid] = t;
+    return;
+  }
+#endif
+  // Epilogue through LDS, one 32-token fragment row at a time.
+  // (1) Raw fp32 accumulators go to this wave's private [token][packed column]
+  //     tile (row pitch padded by 16 bytes: the 16 rows written by 16 lanes
+  //     land in distinct banks).
+  // (2) Each lane owns four consecutive output columns of the tile: their
+  //     scales, bias and adaLN gate are loaded once, the tile's token scales
+  //     are staged in LDS, and a fragment row's residual loads are all issued
+  //     before its math. Every output row is written as one contiguous segment.
+  // The barrier keeps the stage buffers alive until every wave is done with
+  // its MFMAs and publishes the token scales.
+  constexpr int kCols = GLU ? 64 : 128;            // output columns of a wave tile
+  constexpr int kLanesPerRow = kCols / 4;
+  constexpr int kRowsPerPass = 64 / kLanesPerRow;
+  constexpr int kRowIters = 32 / kRowsPerPass;
+  const int64_t nw = n0 + wn * 128;                // first (packed) weight row of the wave tile
+  const int64_t mw = m0 + wm * (BM / 2);           // first token of the wave tile
+  const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
+  const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
+  const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
+  const bool col_ok = c_out < (GLU ? e.N / 2 : e.N);
+  const int64_t np = col_ok ? nw + pc : 0;         // packed weight row (any valid row if unused)
+  const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
+  const float4 sw0 = load_f4_or(e.sw, np, 1.0f);
+  const float4 b0 = load_f4_or(bp, np, 0.0f);
+  const float4 sw1 = GLU ? load_f4_or(e.sw, np + 16, 1.0f) : sw0;
+  const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
+  uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
+  if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
+  if (tid < BM) s_sa[tid] = e.sa ? e.sa[min(m0 + tid, e.M - 1)] : 1.0f;
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  const float swa[4] = {sw0.x, sw0.y, sw0.z, sw0.w}, ba[4] = {b0.x, b0.y, b0.z, b0.w};
+  const float swu[4] = {sw1.x, sw1.y, sw1.z, sw1.w}, bu[4] = {b1.x, b1.y, b1.z, b1.w};
+  const float gta[4] = {__uint_as_float(g2.x << 16), __uint_as_float(g2.x & 0xFFFF0000u),
+                        __uint_as_float(g2.y << 16), __uint_as_float(g2.y & 0xFFFF0000u)};
+  float* tile = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
+  const bool swiglu = (e.flags & IFX_EPI_SWIGLU) != 0;
+  const bool gelu = (e.flags & IFX_EPI_GELU_TANH) != 0;
+  const bool has_gate = (e.flags & IFX_EPI_GATE) != 0;
+  const bool has_res = (e.flags & IFX_EPI_RESIDUAL) != 0;
+  const int r0 = lane / kLanesPerRow;
+
+#pragma unroll
+  for (int j = 0; j < kFM; ++j) {
+#pragma unroll
+    for (int i = 0; i < kFN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float4 res[kRowIters];
+#pragma unroll
+    for (int t = 0; t < kRowIters; ++t) {
+      const int64_t m = mw + j * 32 + r0 + t * kRowsPerPass;
+      res[t] = (col_ok && has_res && m < e.M) ? load_res4(e, m, c_out) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int t = 0; t < kRowIters; ++t) {
+      const int r = r0 + t * kRowsPerPass;
+      const int64_t m = mw + j * 32 + r;
+      if (col_ok && m < e.M) {
+        const float sa = s_sa[wm * (BM / 2) + j * 32 + r];
+        const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
+        const float va[4] = {v.x, v.y, v.z, v.w};
+        const float ra[4] = {res[t].x, res[t].y, res[t].z, res[t].w};
+        float y[4];
+        if constexpr (GLU) {
+          const float4 w = *reinterpret_cast<const float4*>(tile + r * kPitch + pc + 16);
+          const float wa[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float gv = va[u] * sa * swa[u] + ba[u];
+            const float uv = wa[u] * sa * swu[u] + bu[u];
+            y[u] = (swiglu ? silu(gv) : gelu_tanh(gv)) * uv;
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            y[u] = va[u] * sa * swa[u] + ba[u];
+            if (gelu) y[u] = gelu_tanh(y[u]);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (has_gate) y[u] = y[u] * gta[u];
+          if (has_res) y[u] = ra[u] + y[u];
+        }
+        epi_store4(e, m, c_out, y);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 }
 
@@ -480,6 +833,18 @@ int launch_lds(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
   return launch_status();
 }
 
+template <int BM, int KB, int STAGES, int OCC, bool GLU>
+int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e,
+               hipStream_t st) {
+  const int64_t tiles_m = (e.M + BM - 1) / BM;
+  const int64_t tiles_n = (e.N + kBigBN - 1) / kBigBN;
+  if (tiles_m * tiles_n > 0x7FFFFFF0LL) return IFX_ERR_UNSUPPORTED;
+  const TileMap t = make_tile_map(tiles_m, tiles_n);
+  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(256), 0, st, a, lda, w,
+                     ldw, K, t, e);
+  return launch_status();
+}
+
 template <int MB, int NBW>
 void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
                       int64_t K, uint32_t* tickets, float* partials, const Epi& e, hipStream_t st) {
@@ -504,6 +869,19 @@ int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint
 }
 
 constexpr int64_t kSkinnyMaxM = 64;
+
+#ifndef IFX_BIG_BM
+#define IFX_BIG_BM 128
+#endif
+#ifndef IFX_BIG_STAGES
+#define IFX_BIG_STAGES 2
+#endif
+#ifndef IFX_BIG_KB
+#define IFX_BIG_KB 64
+#endif
+#ifndef IFX_BIG_OCC
+#define IFX_BIG_OCC 2
+#endif
 
 }  // namespace
 }  // namespace ifx
@@ -555,6 +933,9 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
     return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, workspace, e, st)
                : launch_skinny<1>(p, A, lda, Wt, ldw, K, workspace, e, st);
   }
+  if (K % IFX_BIG_KB == 0 && M > 128)
+    return glu ? launch_big<IFX_BIG_BM, IFX_BIG_KB, IFX_BIG_STAGES, IFX_BIG_OCC, true>(A, lda, Wt, ldw, K, e, st)
+               : launch_big<IFX_BIG_BM, IFX_BIG_KB, IFX_BIG_STAGES, IFX_BIG_OCC, false>(A, lda, Wt, ldw, K, e, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
 }
