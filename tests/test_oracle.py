@@ -1,0 +1,278 @@
+"""Pins of the CPU oracle (CPU only, no GPU).
+
+The oracle is only trusted because these checks tie it to things it did not
+compute itself:
+  * the reference's known-answer scale (tests/test_sm89_fp8.py:48-56);
+  * torch's own CPU E4M3 cast and the reference's torch formulation of the
+    recipe (tests/test_sm89_fp8.py:242-254, tests/test_dynamic_fp8_pack.py:15-18),
+    over every finite bf16 pattern, the reference's fixed midpoint scales
+    (scripts/qualify_sm89_fp8.py:61), its shapes/magnitudes and non-finite cases;
+  * a brute-force nearest-value search over the OCP E4M3 value set;
+  * closed forms and torch's independent GELU/SiLU for the GEMM reference;
+  * the committed golden fixtures (tests/golden/fp8_golden.npz).
+Each check is chosen so that a plausible slip (true division instead of the
+reciprocal, ties away from zero, a dropped bias, a transposed operand, swapped
+gate/up halves) fails it.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "fp8_golden.npz"
+FIXED_SCALES = (1.0, 1.0 + 2.0 ** -23, 1.0 - 2.0 ** -24, 2.0 ** -16, 1.0 / 448.0)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def all_finite_bf16():
+    pat = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    return pat[torch.isfinite(pat)].contiguous()
+
+
+def torch_recipe(x):
+    """The reference recipe in torch CPU ops, with the device scalar semantics."""
+    scale = x.float().abs().amax(dim=1).clamp_min(1e-12) * torch.tensor(1.0 / 448.0, dtype=torch.float32)
+    q = (x.float() / scale[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).numpy(), scale.numpy()
+
+
+def nan_equal_bytes(a, b):
+    a, b = np.asarray(a, np.uint8), np.asarray(b, np.uint8)
+    na, nb = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F
+    return np.array_equal(na, nb) and np.array_equal(a[~na], b[~nb])
+
+
+# ---------------------------------------------------------------------------
+# scale arithmetic
+# ---------------------------------------------------------------------------
+
+def test_known_answer_scale():
+    _, s = oracle.quant_rows(bits(torch.full((1, 16), 0.0361328125, dtype=torch.bfloat16)))
+    assert s.view(np.uint32)[0] == 0x38A92493
+    # true division (the CPU-only form) would give 0x38A92492: the oracle must not.
+    assert (np.float32(0.0361328125) / np.float32(448.0)).view(np.uint32) == 0x38A92492
+
+
+def test_scale_floor_and_zero_rows():
+    q, s = oracle.quant_rows(np.zeros((2, 16), np.float32))
+    assert np.all(q == 0)
+    assert s.view(np.uint32)[0] == (np.float32(1e-12) * (np.float32(1) / np.float32(448))).view(np.uint32)
+
+
+def test_nonfinite_propagation_matches_torch():
+    for bad in (float("nan"), float("inf"), -float("inf")):
+        x = torch.ones((4, 64), dtype=torch.bfloat16)
+        x[1, 3] = bad
+        q, s = oracle.quant_rows(bits(x))
+        tq, ts = torch_recipe(x)
+        assert np.array_equal(np.isnan(s), np.isnan(ts))
+        assert np.array_equal(s[~np.isnan(s)], ts[~np.isnan(ts)])
+        assert nan_equal_bytes(q, tq)
+
+
+# ---------------------------------------------------------------------------
+# E4M3 rounding
+# ---------------------------------------------------------------------------
+
+def test_decode_table_matches_torch():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    t = oracle.E4M3_VALUES
+    assert np.array_equal(np.isnan(t), np.isnan(codes))
+    assert np.array_equal(t[~np.isnan(t)], codes[~np.isnan(codes)])
+
+
+def test_encode_matches_torch_cast_on_all_bf16_and_midpoints():
+    fin = all_finite_bf16().float().numpy()
+    vals = np.clip(fin, -448, 448)
+    # every E4M3 value, the exact midpoints between neighbours and one fp32 ulp either side
+    pos = np.unique(oracle.E4M3_VALUES[~np.isnan(oracle.E4M3_VALUES)]).astype(np.float32)
+    mids = ((pos[1:].astype(np.float64) + pos[:-1]) / 2).astype(np.float32)
+    near = np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf))])
+    vals = np.concatenate([vals, pos, -pos, near, -near]).astype(np.float32)
+    ours = oracle.e4m3(vals)
+    theirs = torch.from_numpy(vals).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, theirs)
+
+
+def test_encode_is_nearest_ties_to_even_by_brute_force():
+    pos = np.unique(oracle.E4M3_VALUES[~np.isnan(oracle.E4M3_VALUES)]).astype(np.float64)
+    pos = pos[pos >= 0]
+    rng = np.random.default_rng(7)
+    mids = (pos[1:] + pos[:-1]) / 2
+    vals = np.concatenate([rng.uniform(0, 448, 4000), 2.0 ** rng.uniform(-14, -6, 2000), mids, pos]).astype(np.float32)
+    got = oracle.E4M3_VALUES[oracle.e4m3(vals)].astype(np.float64)
+    for v, gv in zip(vals.astype(np.float64), got):
+        d = np.abs(pos - v)
+        best = pos[d == d.min()]
+        if best.size == 2:  # tie: the even code (mantissa LSB 0)
+            codes = [int(np.nonzero(oracle.E4M3_VALUES == b)[0][0]) for b in best]
+            best = [b for b, c in zip(best, codes) if c % 2 == 0]
+        assert gv == best[0], (v, gv, best)
+
+
+def test_sign_and_special_codes():
+    assert list(oracle.e4m3([0.0, -0.0, 448.0, -448.0, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -10, np.nan])) == \
+        [0x00, 0x80, 0x7E, 0xFE, 0x01, 0x00, 0x02, 0x7F]
+
+
+# ---------------------------------------------------------------------------
+# full per-row recipe vs torch's formulation
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,mag", [((40, 2048), 1.0), ((256, 5120), 1.0), ((1, 16), 0.0),
+                                       ((1, 16), 1e-20), ((1, 16), 1e30)])
+def test_rows_match_torch_recipe(shape, mag):
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(shape, generator=g) * mag).to(torch.bfloat16)
+    q, s = oracle.quant_rows(bits(x))
+    tq, ts = torch_recipe(x)
+    assert np.array_equal(s.view(np.uint32), ts.view(np.uint32))
+    assert np.array_equal(q, tq)
+
+
+def test_all_bf16_patterns_match_torch_recipe():
+    fin = all_finite_bf16()
+    for x in (fin.reshape(1, -1), fin.reshape(255, 256)):
+        q, s = oracle.quant_rows(bits(x))
+        tq, ts = torch_recipe(x)
+        assert np.array_equal(s.view(np.uint32), ts.view(np.uint32))
+        assert np.array_equal(q, tq)
+
+
+@pytest.mark.parametrize("scale", FIXED_SCALES)
+def test_fixed_scale_pack_matches_torch(scale):
+    fin = all_finite_bf16()
+    st = torch.tensor([scale], dtype=torch.float32)
+    tq = (fin.float() / st).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.pack_fixed(bits(fin), float(st.item())), tq)
+
+
+def test_per_tensor_matches_reference_formulation():
+    # tests/test_dynamic_fp8_pack.py:15-18, with the device reciprocal scale
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn((40, 2048), generator=g).to(torch.bfloat16)
+    q, s = oracle.quant_tensor(bits(x))
+    es = x.abs().amax().float().clamp_min(1e-12).reshape(1) * torch.tensor(1.0 / 448.0)
+    eq = (x.float() / es).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert s.view(np.uint32)[0] == es.numpy().view(np.uint32)[0]
+    assert np.array_equal(q, eq)
+
+
+def test_f32_weights_match_quantize_weight_recipe():
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn((32, 1000), generator=g) * 0.02
+    w[4] = 0
+    q, s = oracle.quant_rows(w.numpy())
+    tq, ts = torch_recipe(w)
+    assert np.array_equal(q, tq) and np.array_equal(s.view(np.uint32), ts.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# GEMM reference
+# ---------------------------------------------------------------------------
+
+def _small(seed=3, M=6, N=32, K=64):
+    g = torch.Generator().manual_seed(seed)
+    qa, sa = oracle.quant_rows(bits(torch.randn((M, K), generator=g).to(torch.bfloat16)))
+    qw, sw = oracle.quant_rows((torch.randn((N, K), generator=g) * 0.02).numpy())
+    return qa, sa, qw, sw, g
+
+
+def test_ref_linear_matches_fp64_brute_force():
+    qa, sa, qw, sw, _ = _small()
+    A = oracle.e4m3_decode(qa).astype(np.float64) * sa[:, None]
+    W = oracle.e4m3_decode(qw).astype(np.float64) * sw[:, None]
+    exact = np.array([[sum(A[m, k] * W[n, k] for k in range(A.shape[1])) for n in range(W.shape[0])]
+                      for m in range(A.shape[0])])
+    ref = oracle.ref_linear(qa, sa, qw, sw)
+    assert np.allclose(ref, exact, rtol=1e-5, atol=1e-6)
+    # a transposed operand or missing row scale is caught by the acceptance metric
+    bad = oracle.ref_linear(qa, None, qw, sw)
+    assert oracle.parity_stats(bad, ref)[0] > 2e-2
+
+
+def test_ref_linear_identity_closed_form():
+    # W = I (scale 1): out = dequantized activations exactly
+    K = 32
+    qa, sa, _, _, _ = _small(K=K, N=K)
+    eye = np.zeros((K, K), np.uint8)
+    eye[np.arange(K), np.arange(K)] = 0x38  # e4m3 1.0
+    out = oracle.ref_linear(qa, sa, eye, np.ones(K, np.float32))
+    assert np.array_equal(out, (oracle.e4m3_decode(qa) * sa[:, None]).astype(np.float32))
+
+
+def test_activations_match_torch():
+    x = np.linspace(-8, 8, 4001, dtype=np.float32)
+    tg = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    ts = torch.nn.functional.silu(torch.from_numpy(x)).numpy()
+    assert np.allclose(oracle.gelu_tanh(x), tg, rtol=1e-5, atol=1e-6)
+    assert np.allclose(oracle.silu(x), ts, rtol=1e-5, atol=1e-6)
+    assert oracle.gelu_tanh(np.float32(0.0)) == 0.0
+
+
+def test_glu_halves_and_epilogue_order():
+    qa, sa, qw, sw, g = _small(N=64)
+    y = oracle.ref_linear(qa, sa, qw, sw)
+    gg, uu = torch.from_numpy(y[:, :32]), torch.from_numpy(y[:, 32:])
+    geglu = (torch.nn.functional.gelu(gg, approximate="tanh") * uu).numpy()
+    assert np.allclose(oracle.ref_linear(qa, sa, qw, sw, act="geglu"), geglu, rtol=1e-6, atol=1e-7)
+    swapped = (torch.nn.functional.gelu(uu, approximate="tanh") * gg).numpy()
+    assert oracle.parity_stats(swapped, geglu)[0] > 2e-2
+    # residual + gate * (y + bias): the gate scales the projection, not the residual
+    bias = np.linspace(-1, 1, 64).astype(np.float32)
+    res = np.ones((y.shape[0], 64), np.float32)
+    gate = np.full(64, 0.5, np.float32)
+    got = oracle.ref_linear(qa, sa, qw, sw, bias=bias, residual=res, gate=gate)
+    assert np.allclose(got, 1.0 + 0.5 * (y + bias), rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures (tests/golden/make_golden.py)
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)
+
+
+def test_golden_rows(golden):
+    names = [k[:-2] for k in golden.files if k.endswith("_q") and not k.startswith("fixed")]
+    assert {"kat", "allbf16", "allbf16_rows", "act_c1", "act_c5h", "weight_f32"} <= set(names)
+    fin = bits(all_finite_bf16())
+    for n in names:
+        x = golden[f"{n}_x"] if f"{n}_x" in golden.files else (fin.reshape(1, -1) if n == "allbf16"
+                                                               else fin.reshape(255, 256))
+        q, s = oracle.quant_rows(x)
+        assert np.array_equal(q, golden[f"{n}_q"]), n
+        assert np.array_equal(s.view(np.uint32), golden[f"{n}_s"].view(np.uint32)), n
+    assert golden["kat_s"].view(np.uint32)[0] == 0x38A92493
+
+
+def test_golden_fixed_scales(golden):
+    fin = bits(all_finite_bf16())
+    for i in range(len(FIXED_SCALES)):
+        assert np.array_equal(oracle.pack_fixed(fin, float(golden[f"fixed{i}_scale"][0])), golden[f"fixed{i}_q"])
+
+
+def test_golden_gemm(golden):
+    G = golden
+    common = (G["gemm_qa"], G["gemm_sa"], G["gemm_qw"], G["gemm_sw"])
+    res = oracle.bf16_to_f32(G["gemm_res"])
+    gate = oracle.bf16_to_f32(G["gemm_gate"])
+    assert np.array_equal(oracle.ref_linear(*common, bias=G["gemm_bias"]), G["gemm_plain"])
+    assert np.array_equal(oracle.ref_linear(*common, bias=G["gemm_bias"], act="gelu_tanh"), G["gemm_gelu"])
+    assert np.array_equal(oracle.ref_linear(*common, act="geglu"), G["gemm_geglu"])
+    assert np.array_equal(oracle.ref_linear(*common, act="swiglu"), G["gemm_swiglu"])
+    assert np.array_equal(oracle.ref_linear(*common, bias=G["gemm_bias"], residual=res, gate=gate),
+                          G["gemm_gated_res"])
+
+
+def test_f32_to_bf16_rounding_matches_torch():
+    x = np.random.default_rng(3).standard_normal(100000).astype(np.float32) * 1000
+    assert np.array_equal(oracle.f32_to_bf16(x), bits(torch.from_numpy(x).to(torch.bfloat16)))
