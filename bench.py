@@ -18,7 +18,7 @@ around a graph of back-to-back launches of that kernel alone, on the stream it
 runs on, and gives the "roofline" object.
 
 The CPU baseline runs the reference's PyTorch CPU FP8 path (oracle/cpu_path.py)
-on the host cores for one C2 unit.
+on the host cores: whole C2 units, repeated until about 10 s of CPU time.
 """
 from __future__ import annotations
 
@@ -115,7 +115,7 @@ def summarize(wl, m):
     return res
 
 
-def cpu_baseline(seconds_hint=True):
+def cpu_baseline(min_seconds=10.0):
     """Reference CPU FP8 path for one C2 unit (4 flow steps = 8 projections)."""
     import torch
     from oracle import cpu_path
@@ -128,16 +128,32 @@ def cpu_baseline(seconds_hint=True):
     res = torch.randn((M, D), generator=g).to(torch.bfloat16)
     q1, s1 = cpu_path.quant_rows(w1)
     q2, s2 = cpu_path.quant_rows(w2)
-    t0 = time.perf_counter()
-    cpu_path.c2_unit(xs, q1, s1, q2, s2, res)
-    dt = time.perf_counter() - t0
+    cpu_path.c2_unit(xs, q1, s1, q2, s2, res)  # warm-up (oneDNN primitive creation)
+    units, t0 = 0, time.perf_counter()
+    while True:  # a bounded sample: whole units until ~min_seconds of CPU work
+        cpu_path.c2_unit(xs, q1, s1, q2, s2, res)
+        units += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or units >= 100000:
+            break
+    dt /= units
     gemms = [Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True)]
     nbytes = 4 * (sum(x.bytes for x in gemms) + quant_bytes(M, D) + quant_bytes(M, FF))
     return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port", "seconds": round(dt, 2),
-            "sample": "one full C2 unit (4 flow steps x [quant, 16x1536->6144 GELU, quant, 16x6144->1536 +res]) "
-                      "via torch._scaled_mm (oneDNN) on the host CPU, reference GI decomposition",
-            "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count()}
+            "kind": "port", "seconds_per_unit": round(dt, 4), "units_timed": units,
+            "sample": f"{units} full C2 units (4 flow steps x [quant, 16x1536->6144 GELU, quant, 16x6144->1536 "
+                      "+res]) via torch._scaled_mm (oneDNN) on the host CPU, reference GI decomposition",
+            "cpu": _cpu_model(), "os_cpu_count": os.cpu_count()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def main():

@@ -27,13 +27,9 @@
 //    the fragment reads are bank-conflict free), global loads of stage k+1 in
 //    flight while stage k runs on the matrix cores, epilogue from registers.
 //  * gemm_skinny (M <= 64): bandwidth-bound on the weight stream. One workgroup
-//    owns 16 (32 for GLU) weight rows and a K range; every wave streams weight
-//    fragments straight from HBM into MFMA registers (no LDS staging), partial
-//    sums are reduced across waves in LDS and, when K is split across
-//    workgroups, across workgroups through a workspace: the last workgroup to
-//    finish a row group (atomic ticket) adds the partials in split order and
-//    runs the epilogue, so results are deterministic; it also resets the ticket,
-//    so the workspace stays zeroed between calls.
+//    owns 16 (32 for GLU) weight rows; its waves split K, stream weight
+//    fragments straight from HBM into MFMA registers (no LDS staging), and their
+//    partial sums are added in LDS in a fixed order (deterministic).
 
 #include "ifx_abi.h"
 #include "ifx_device.h"
@@ -643,69 +639,56 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (M <= 64): weight streaming, split-K
+// Skinny kernel (M <= 64): weight streaming
 // ---------------------------------------------------------------------------
+//
+// One workgroup owns 16 weight rows (32 for GLU: a gate block and its up block)
+// for the whole of K; its WAVES waves split K between them (wave w takes 128-byte
+// K steps w, w+WAVES, ...), each loading kSkUnroll steps of weight fragments
+// (nontemporal: read once per call) and token fragments before issuing their
+// MFMAs, and the partial sums are added in LDS in wave order. No workgroup
+// waits for another, so the kernel needs no device-scope fences or workspace.
 
-constexpr int kSkWaves = 4;
 constexpr int kSkUnroll = 4;  // K steps whose loads are issued together per wave
 
 struct SkinnyPlan {
-  int mb;         // 16-token blocks (1..4)
-  int nbw;        // 16-row weight blocks per workgroup (1, or 2 for GLU)
-  int64_t groups; // workgroups along N
-  int splits;     // workgroups along K
-  int64_t ksteps; // 128-byte K steps in total
-  int64_t steps_per_split;
-  size_t ws_bytes;
+  int mb;          // 16-token blocks (1..4)
+  int nbw;         // 16-row weight blocks per workgroup (1, or 2 for GLU)
+  int64_t groups;  // workgroups
+  int waves;       // waves per workgroup (4, 8 or 16)
 };
-
-// Workspace layout (fixed for every shape, so a call never finds another call's
-// partial sums where its tickets live): [tickets: kTicketBytes][partials].
-// Split-K is only used when there are fewer than kMaxTicketGroups row groups.
-constexpr int64_t kMaxTicketGroups = 1024;
-constexpr size_t kTicketBytes = kMaxTicketGroups * sizeof(uint32_t);
 
 __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu) {
   SkinnyPlan p{};
   p.mb = static_cast<int>((M + 15) / 16);
   p.nbw = glu ? 2 : 1;
   p.groups = N / (16 * p.nbw);
-  p.ksteps = (K + kBK - 1) / kBK;
-  // Aim for >= 256 workgroups (one per CU) while giving every wave at least
-  // two K steps of its own.
-  int64_t s = (256 + p.groups - 1) / p.groups;
-  const int64_t smax = p.ksteps / (2 * kSkWaves);
-  if (s > smax) s = smax;
-  if (s < 1 || p.groups > kMaxTicketGroups) s = 1;
-  p.steps_per_split = (p.ksteps + s - 1) / s;
-  p.splits = static_cast<int>((p.ksteps + p.steps_per_split - 1) / p.steps_per_split);
-  if (p.splits > 1) {
-    const size_t partial = static_cast<size_t>(p.splits) * p.groups * p.nbw * p.mb * 64 * 4 * sizeof(float);
-    p.ws_bytes = kTicketBytes + partial;
-  }
+  const int64_t ksteps = (K + kBK - 1) / kBK;
+  // Enough waves that every wave has at most kSkUnroll K steps (one batch of
+  // loads in flight), within the LDS budget of the cross-wave reduction.
+  int w = 4;
+#ifdef IFX_SK_WAVES
+  w = IFX_SK_WAVES;
+  while (w * p.nbw * p.mb > 32) w /= 2;
+#else
+  while (w < 16 && ksteps > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
+#endif
+  p.waves = w;
   return p;
 }
 
-template <int MB, int NBW>
-__global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
-                                                             const uint8_t* __restrict__ W, int64_t ldw,
-                                                             int64_t K, int64_t steps_per_split, int splits,
-                                                             uint32_t* tickets, float* partials, Epi e) {
-  __shared__ v4f red[kSkWaves][NBW][MB][64];
-  __shared__ int last_flag;
+template <int MB, int NBW, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
+                                                          const uint8_t* __restrict__ W, int64_t ldw,
+                                                          int64_t K, Epi e) {
+  __shared__ v4f red[WAVES][NBW][MB][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t grp = blockIdx.x;
-  const int split = blockIdx.y;
-  const int64_t nrow0 = grp * (16 * NBW);
+  const int64_t nrow0 = static_cast<int64_t>(blockIdx.x) * (16 * NBW);
   const int frow = lane & 15;
   const int g = lane >> 4;
-
   const int64_t ksteps = (K + kBK - 1) / kBK;
-  const int64_t s_begin = split * steps_per_split;
-  int64_t s_end = s_begin + steps_per_split;
-  s_end = s_end < ksteps ? s_end : ksteps;
 
   const uint8_t* wrow[NBW];
 #pragma unroll
@@ -714,8 +697,35 @@ __global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny(const uint8_t* __re
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
     int64_t m = j * 16 + frow;
-    m = m < e.M ? m : e.M - 1;
+    m = m < e.M ? m : e.M - 1;  // rows past M are computed, never stored
     arow[j] = A + m * lda + g * 32;
+  }
+
+  // Epilogue operands of the lanes that will finish token block j = wave,
+  // fetched now so their latency hides under the weight stream.
+  const int64_t m_epi = wave < MB ? wave * 16 + frow : e.M;
+  const int64_t mc = min(m_epi, e.M - 1);
+  const int64_t c_epi = NBW == 2 ? (nrow0 >> 5) * 16 + 4 * g : nrow0 + 4 * g;  // output column
+  float sa_epi = 1.0f, sw_epi[NBW][4], b_epi[NBW][4], gate_epi[4] = {1.f, 1.f, 1.f, 1.f}, res_epi[4] = {0.f, 0.f, 0.f, 0.f};
+  if (wave < MB) {
+    if (e.sa) sa_epi = e.sa[mc];
+    const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) {
+      const float4 w4 = load_f4_or(e.sw, nrow0 + b * 16 + 4 * g, 1.0f);
+      const float4 b4 = load_f4_or(bp, nrow0 + b * 16 + 4 * g, 0.0f);
+      sw_epi[b][0] = w4.x; sw_epi[b][1] = w4.y; sw_epi[b][2] = w4.z; sw_epi[b][3] = w4.w;
+      b_epi[b][0] = b4.x; b_epi[b][1] = b4.y; b_epi[b][2] = b4.z; b_epi[b][3] = b4.w;
+    }
+    if (e.flags & IFX_EPI_GATE) {
+      const uint2 g2 = *reinterpret_cast<const uint2*>(e.gate + c_epi);
+      gate_epi[0] = __uint_as_float(g2.x << 16); gate_epi[1] = __uint_as_float(g2.x & 0xFFFF0000u);
+      gate_epi[2] = __uint_as_float(g2.y << 16); gate_epi[3] = __uint_as_float(g2.y & 0xFFFF0000u);
+    }
+    if (e.flags & IFX_EPI_RESIDUAL) {
+      const float4 r4 = load_res4(e, mc, c_epi);
+      res_epi[0] = r4.x; res_epi[1] = r4.y; res_epi[2] = r4.z; res_epi[3] = r4.w;
+    }
   }
 
   v4f acc[NBW][MB];
@@ -724,31 +734,24 @@ __global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny(const uint8_t* __re
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[b][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // Wave w takes K steps s_begin+w, +kSkWaves, ... in groups of kSkUnroll whose
-  // loads are all issued before the first MFMA of the group.
-  for (int64_t s0 = s_begin + wave; s0 < s_end; s0 += kSkWaves * kSkUnroll) {
+  for (int64_t s0 = wave; s0 < ksteps; s0 += WAVES * kSkUnroll) {
     v8i wf[kSkUnroll][NBW];
     v8i af[kSkUnroll][MB];
 #pragma unroll
     for (int u = 0; u < kSkUnroll; ++u) {
-      const int64_t s = s0 + u * kSkWaves;
+      const int64_t s = s0 + u * WAVES;
       const int64_t k0 = s * kBK + g * 32;
-      const bool ok = s < s_end;
-      const bool lo = ok && k0 < K;       // K % 16 == 0: each 16-byte half is all-in or all-out
-      const bool hi = ok && k0 + 16 < K;
+      const bool lo = s < ksteps && k0 < K;  // K % 16 == 0: a 16-byte half is all in or all out
+      const bool hi = s < ksteps && k0 + 16 < K;
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
         const uint8_t* p = wrow[b] + s * kBK;
-        const v4i x0 = lo ? ld16_nt(p) : v4i{0, 0, 0, 0};
-        const v4i x1 = hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0};
-        wf[u][b] = cat8(x0, x1);
+        wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
       }
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
         const uint8_t* p = arow[j] + s * kBK;
-        const v4i x0 = lo ? ld16(p) : v4i{0, 0, 0, 0};
-        const v4i x1 = hi ? ld16(p + 16) : v4i{0, 0, 0, 0};
-        af[u][j] = cat8(x0, x1);
+        af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
       }
     }
 #pragma unroll
@@ -759,61 +762,46 @@ __global__ __launch_bounds__(kSkWaves * 64) void gemm_skinny(const uint8_t* __re
         for (int j = 0; j < MB; ++j) acc[b][j] = mfma16(wf[u][b], af[u][j], acc[b][j]);
   }
 
-  // Cross-wave reduction in LDS (fixed order: wave 0..3).
+  // Cross-wave reduction in LDS, fixed order (wave 0, 1, ...): deterministic.
 #pragma unroll
   for (int b = 0; b < NBW; ++b)
 #pragma unroll
     for (int j = 0; j < MB; ++j) red[wave][b][j][lane] = acc[b][j];
   __syncthreads();
-  // Wave w finalizes fragment pairs (b, j) with (b*MB + j) % kSkWaves == w.
-  constexpr int kFrags = NBW * MB;
-
-  if (splits > 1) {
-    // Publish this split's partial sums, then take a ticket.
-    for (int f = wave; f < kFrags; f += kSkWaves) {
-      const int b = f / MB, j = f % MB;
-      v4f s = red[0][b][j][lane];
+  // wave w finishes token block j = w (for w < MB) with the operands it
+  // prefetched before the K loop
+  if (wave < MB) {
+    const int j = wave;
+    v4f s[NBW];
 #pragma unroll
-      for (int w = 1; w < kSkWaves; ++w) s += red[w][b][j][lane];
-      float* dst = partials + ((((static_cast<int64_t>(split) * gridDim.x + grp) * NBW + b) * MB + j) * 64 + lane) * 4;
-      *reinterpret_cast<v4f*>(dst) = s;
+    for (int b = 0; b < NBW; ++b) {
+      s[b] = red[0][b][j][lane];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) s[b] += red[w][b][j][lane];
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t t = atomicAdd(tickets + grp, 1u);
-      last_flag = (t == static_cast<uint32_t>(splits - 1));
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    for (int f = wave; f < kFrags; f += kSkWaves) {
-      const int b = f / MB, j = f % MB;
-      v4f s = v4f{0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < splits; ++sp) {
-        const float* src = partials + ((((static_cast<int64_t>(sp) * gridDim.x + grp) * NBW + b) * MB + j) * 64 + lane) * 4;
-        s += __builtin_nontemporal_load(reinterpret_cast<const v4f*>(src));
+    if (m_epi < e.M) {
+      float y[4];
+      if constexpr (NBW == 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gv = s[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
+          const float uv = s[1][r] * sa_epi * sw_epi[1][r] + b_epi[1][r];
+          y[r] = ((e.flags & IFX_EPI_SWIGLU) ? silu(gv) : gelu_tanh(gv)) * uv;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          y[r] = s[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
+          if (e.flags & IFX_EPI_GELU_TANH) y[r] = gelu_tanh(y[r]);
+        }
       }
-      red[0][b][j][lane] = s;
-    }
-    if (tid == 0) tickets[grp] = 0u;
-  } else {
-    for (int f = wave; f < kFrags; f += kSkWaves) {
-      const int b = f / MB, j = f % MB;
-      v4f s = red[0][b][j][lane];
 #pragma unroll
-      for (int w = 1; w < kSkWaves; ++w) s += red[w][b][j][lane];
-      red[0][b][j][lane] = s;
+      for (int r = 0; r < 4; ++r) {
+        if (e.flags & IFX_EPI_GATE) y[r] = y[r] * gate_epi[r];
+        if (e.flags & IFX_EPI_RESIDUAL) y[r] = res_epi[r] + y[r];
+      }
+      epi_store4(e, m_epi, c_epi, y);
     }
-  }
-  __syncthreads();
-  const int64_t m_base = frow;
-  if constexpr (NBW == 2) {
-    // GLU: block 0 = gate rows, block 1 = up rows.
-    for (int j = wave; j < MB; j += kSkWaves)
-      epi_store_glu(e, red[0][0][j][lane], red[0][1][j][lane], nrow0 + 4 * g, m_base + j * 16);
-  } else {
-    for (int j = wave; j < MB; j += kSkWaves) epi_store(e, red[0][0][j][lane], nrow0 + 4 * g, m_base + j * 16);
   }
 }
 
@@ -845,25 +833,29 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
   return launch_status();
 }
 
+template <int MB, int NBW, int WAVES>
+void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
+                     const Epi& e, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES>), dim3(static_cast<unsigned>(p.groups)), dim3(WAVES * 64), 0,
+                     st, a, lda, w, ldw, K, e);
+}
+
 template <int MB, int NBW>
-void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
-                      int64_t K, uint32_t* tickets, float* partials, const Epi& e, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_skinny<MB, NBW>), dim3(static_cast<unsigned>(p.groups), p.splits),
-                     dim3(kSkWaves * 64), 0, st, a, lda, w, ldw, K, p.steps_per_split, p.splits, tickets,
-                     partials, e);
+void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
+                      const Epi& e, hipStream_t st) {
+  if (p.waves >= 16 && 16 * NBW * MB <= 32) launch_skinny_w<MB, NBW, 16>(p, a, lda, w, ldw, K, e, st);
+  else if (p.waves >= 8 && 8 * NBW * MB <= 32) launch_skinny_w<MB, NBW, 8>(p, a, lda, w, ldw, K, e, st);
+  else launch_skinny_w<MB, NBW, 4>(p, a, lda, w, ldw, K, e, st);
 }
 
 template <int NBW>
-int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw,
-                  int64_t K, void* ws, const Epi& e, hipStream_t st) {
-  uint32_t* tickets = static_cast<uint32_t*>(ws);
-  float* partials = nullptr;
-  if (p.splits > 1) partials = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kTicketBytes);
+int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
+                  const Epi& e, hipStream_t st) {
   switch (p.mb) {
-    case 1: launch_skinny_mb<1, NBW>(p, a, lda, w, ldw, K, tickets, partials, e, st); break;
-    case 2: launch_skinny_mb<2, NBW>(p, a, lda, w, ldw, K, tickets, partials, e, st); break;
-    case 3: launch_skinny_mb<3, NBW>(p, a, lda, w, ldw, K, tickets, partials, e, st); break;
-    default: launch_skinny_mb<4, NBW>(p, a, lda, w, ldw, K, tickets, partials, e, st); break;
+    case 1: launch_skinny_mb<1, NBW>(p, a, lda, w, ldw, K, e, st); break;
+    case 2: launch_skinny_mb<2, NBW>(p, a, lda, w, ldw, K, e, st); break;
+    case 3: launch_skinny_mb<3, NBW>(p, a, lda, w, ldw, K, e, st); break;
+    default: launch_skinny_mb<4, NBW>(p, a, lda, w, ldw, K, e, st); break;
   }
   return launch_status();
 }
@@ -891,9 +883,10 @@ using namespace ifx;
 extern "C" {
 
 size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue) {
-  if (M <= 0 || M > kSkinnyMaxM || N <= 0 || K <= 0) return 0;
-  const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
-  return skinny_plan(M, N, K, glu).ws_bytes;
+  // No kernel variant of this build needs a workspace; the argument pair is
+  // part of the ABI so a split-K variant can use one without a signature change.
+  (void)M; (void)N; (void)K; (void)epilogue;
+  return 0;
 }
 
 int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
@@ -929,9 +922,8 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
 
   if (M <= kSkinnyMaxM) {
     const SkinnyPlan p = skinny_plan(M, N, K, glu);
-    if (p.splits > 1 && (!workspace || ws_bytes < p.ws_bytes)) return IFX_ERR_WORKSPACE;
-    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, workspace, e, st)
-               : launch_skinny<1>(p, A, lda, Wt, ldw, K, workspace, e, st);
+    (void)workspace; (void)ws_bytes;
+    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, st) : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, st);
   }
   if (K % IFX_BIG_KB == 0 && M > 128)
     return glu ? launch_big<IFX_BIG_BM, IFX_BIG_KB, IFX_BIG_STAGES, IFX_BIG_OCC, true>(A, lda, Wt, ldw, K, e, st)

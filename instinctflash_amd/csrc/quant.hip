@@ -229,7 +229,14 @@ int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q,
   }
   if (M > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
   const int64_t nvec = K / 8;
-  if (vec_ok && K % 8 == 0 && nvec <= 2048) {
+  if (vec_ok && K % 8 == 0 && nvec <= 2048 && M < 256) {
+    // Few rows: latency-bound, so give every row a whole 256-lane block (one
+    // or two loads per lane in flight) instead of packing rows per block.
+    if (nvec <= 256) launch_vec<256, 1>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 512) launch_vec<256, 2>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 1024) launch_vec<256, 4>(src, M, K, q, ldq, scale, st);
+    else launch_vec<256, 8>(src, M, K, q, ldq, scale, st);
+  } else if (vec_ok && K % 8 == 0 && nvec <= 2048) {
     if (nvec <= 64) launch_vec<64, 1>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 128) launch_vec<64, 2>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 256) launch_vec<64, 4>(src, M, K, q, ldq, scale, st);

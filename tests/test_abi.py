@@ -51,7 +51,7 @@ def test_abi_version_and_status_strings(lib):
 
 
 def test_workspace_queries(lib):
-    # large-M GEMMs and single-split skinny plans need no workspace
+    # no variant of this build needs a workspace
     assert lib.ifx_fp8_linear_workspace_size(8192, 3072, 3072, 0) == 0
     assert lib.ifx_fp8_linear_workspace_size(16, 6144, 1536, 0) == 0
     assert lib.ifx_quant_tensor_workspace_size(0) == 0
