@@ -141,9 +141,11 @@ int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const flo
  * Contract: N % 16 == 0 (N % 32 for GLU), K % 16 == 0, a/w/out 16-byte aligned,
  * lda/ldw multiples of 16, ldo/ldr multiples of 8. sa: f32 [M] or NULL,
  * sw: f32 [N] or NULL, bias: f32 [N] or NULL, gate: bf16 [N_out] or NULL.
- * workspace / ws_bytes: reserved for split-K variants. Every variant of this
- * build reports ifx_fp8_linear_workspace_size() == 0 and ignores them (NULL, 0
- * is valid).
+ * workspace: at least ifx_fp8_linear_workspace_size(M,N,K,epilogue) bytes of
+ * 16-byte aligned device memory. It holds split-K partial sums (fp32) when the
+ * output has too few 256 x 256 tiles to fill the GPU; the size is 0 (NULL
+ * allowed) otherwise. No initialization is needed and nothing is kept between
+ * calls; calls that may overlap must not share a workspace.
  * With sa = sw = NULL and epilogue 0 this is the raw-accumulator GEMM of
  * instinctflash/kernels/fp8.py:50-53 `gemm` (torch._scaled_mm with unit scales,
  * bf16 out). With scales and flags it fuses the consumers

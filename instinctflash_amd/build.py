@@ -34,6 +34,8 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
+    # the DMA helper's inline asm sets M0 (a reserved register) on purpose
+    "-Wno-inline-asm",
 ]
 
 

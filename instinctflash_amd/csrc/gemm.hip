@@ -333,8 +333,8 @@ __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __re
 // Large-M kernel: direct-to-LDS multi-stage ring, 32x32x64 matrix cores
 // ---------------------------------------------------------------------------
 //
-// Workgroup tile: 256 weight rows x BM tokens, 4 waves in a 2 x 2 grid, wave
-// tile 128 x BM/2, built from v_mfma_f32_32x32x64_f8f6f4 (the 32x32 form keeps
+// Workgroup tile: 256 weight rows x BM tokens, 2 x BM/64 waves (2 along weight
+// rows), wave tile 128 x 64, built from v_mfma_f32_32x32x64_f8f6f4 (the 32x32 form keeps
 // the matrix pipe ~97% busy from a single wave per SIMD on gfx950; the 16x16x128
 // form reaches ~75% there). Operand roles as in the other kernels: weights are
 // source 0, so a lane of a 32x32 fragment holds, for q = 0..3, the four
@@ -359,7 +359,24 @@ __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __re
 // for the loads that are meant to stay in flight.
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* global_void_ptr;
+
+// LDS byte offset of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)(p)));
+}
+
+// One global_load_lds_dwordx4: 64 lanes x 16 bytes from `src` (per lane) into
+// the 1 KB LDS block at byte offset `lds` (wave-uniform, via M0). Written as
+// inline asm on purpose: the compiler does not know this instruction writes
+// LDS, so it does not put an s_waitcnt vmcnt(0) in front of every later LDS
+// read "in case they alias" -- that wait would also drain the loads of the
+// stages that are meant to stay in flight. The kernel orders the DMA and the
+// LDS reads itself (s_waitcnt vmcnt(N) + s_barrier before each stage is read;
+// vector-memory loads complete in issue order, so the compiler's own vmcnt
+// counts for other loads stay conservative).
+__device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+}
 
 constexpr int kBigBN = 256;
 
@@ -386,14 +403,19 @@ struct Swz {
 // groups of `group_m` token-tile rows, walking the weight tiles inside a group
 // (tile (tm, tn) with tm fastest), so the ~32 tiles an XCD runs at once form a
 // compact block that shares weight and token panels in that XCD's L2.
+// With split-K the logical index also carries the K slice (slowest), so the
+// slices of one tile are spread over all XCDs.
 struct TileMap {
-  int tiles_m, tiles_n, group_m, per_xcd;
+  int tiles_m, tiles_n, group_m, per_xcd, ksplit;
 };
 
-__device__ __forceinline__ bool map_tile(const TileMap& t, int& tm, int& tn) {
+__device__ __forceinline__ bool map_tile(const TileMap& t, int& tm, int& tn, int& split) {
   const int b = blockIdx.x;
-  const int logical = (b & 7) * t.per_xcd + (b >> 3);
-  if (logical >= t.tiles_m * t.tiles_n) return false;
+  int logical = (b & 7) * t.per_xcd + (b >> 3);
+  const int tiles = t.tiles_m * t.tiles_n;
+  if (logical >= tiles * t.ksplit) return false;
+  split = logical / tiles;
+  logical -= split * tiles;
   const int per_group = t.group_m * t.tiles_n;
   const int grp = logical / per_group;
   const int first_m = grp * t.group_m;
@@ -404,14 +426,24 @@ __device__ __forceinline__ bool map_tile(const TileMap& t, int& tm, int& tn) {
   return true;
 }
 
-__host__ inline TileMap make_tile_map(int64_t tiles_m, int64_t tiles_n) {
+__host__ inline TileMap make_tile_map(int64_t tiles_m, int64_t tiles_n, int ksplit = 1) {
   TileMap t;
   t.tiles_m = static_cast<int>(tiles_m);
   t.tiles_n = static_cast<int>(tiles_n);
   t.group_m = static_cast<int>(tiles_m < 4 ? tiles_m : 4);
-  t.per_xcd = static_cast<int>((tiles_m * tiles_n + 7) / 8);
+  t.ksplit = ksplit;
+  t.per_xcd = static_cast<int>((tiles_m * tiles_n * ksplit + 7) / 8);
   return t;
 }
+
+// Split-K partial sums: raw fp32 accumulators of K slice s at
+// base + (s * M + m) * ld + n (n = packed weight row), written by gemm_big and
+// summed in slice order by splitk_reduce.
+struct Partials {
+  float* base;
+  int64_t ld;
+  int64_t kstages;  // K stages per slice
+};
 
 __device__ __forceinline__ v16f mfma32(const v8i& w, const v8i& a, const v16f& c) {
   // cbsz = blgp = 0: both operands FP8 E4M3 (OCP); no block scales.
@@ -430,21 +462,23 @@ __device__ __forceinline__ v4f quad(const v16f& v, int q) {
 }
 
 template <int BM, int KB, int STAGES, int OCC, bool GLU>
-__global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
+__global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
                                                      const uint8_t* __restrict__ W, int64_t ldw, int64_t K,
-                                                     TileMap tmap, Epi e) {
+                                                     TileMap tmap, Epi e, Partials part) {
   using S = Swz<KB>;
   constexpr int kRows = kBigBN + BM;
   constexpr int kStage = kRows * KB;
   constexpr int kRowsPerDma = 1024 / KB;           // rows one DMA instruction fills
-  constexpr int kLoads = kRows / kRowsPerDma / 4;  // DMA instructions per wave per stage
+  constexpr int kWM = BM / 64;                     // waves along tokens (2 along weight rows)
+  constexpr int kWaves = 2 * kWM;
+  constexpr int kLoads = kRows / kRowsPerDma / kWaves;  // DMA instructions per wave per stage
   constexpr int kFN = 4;                           // 32-row weight fragments per wave (128 rows)
-  constexpr int kFM = BM / 64;                     // 32-token fragments per wave
+  constexpr int kFM = 2;                           // 32-token fragments per wave (64 tokens)
   constexpr int kHalves = KB / 64;                 // 32x32x64 K steps per stage
-  static_assert(BM % 64 == 0 && kRows % (4 * kRowsPerDma) == 0, "tile");
+  static_assert(BM % 64 == 0 && kRows % (kWaves * kRowsPerDma) == 0, "tile");
   static_assert(KB == 64 || KB == 128, "stage depth");
   constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
-  constexpr int kEpiBytes = 4 * 32 * kPitch * 4;
+  constexpr int kEpiBytes = kWaves * 32 * kPitch * 4;
   constexpr int kSmem = STAGES * kStage > kEpiBytes ? STAGES * kStage : kEpiBytes;
   static_assert(OCC * kSmem <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
@@ -453,14 +487,16 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wn = wave >> 1;  // weight-row half
-  const int wm = wave & 1;   // token-row half
+  const int wn = wave / kWM;  // weight-row half
+  const int wm = wave % kWM;  // 64-token slice
 
-  int tm, tn;
-  if (!map_tile(tmap, tm, tn)) return;
+  int tm, tn, split;
+  if (!map_tile(tmap, tm, tn, split)) return;
   const int64_t n0 = static_cast<int64_t>(tn) * kBigBN;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
-  const int nk = static_cast<int>(K / KB);
+  // this workgroup's K stages: [kt0, kt0 + nk)
+  const int kt0 = static_cast<int>(split * part.kstages);
+  const int nk = static_cast<int>(min(static_cast<int64_t>(K / KB) - kt0, part.kstages));
 
   // DMA load i of a stage covers rows kRowsPerDma*blk .. +kRowsPerDma-1
   // (blk = wave*kLoads + i; weight rows first, then token rows). Rows past N/M
@@ -468,8 +504,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
   // VGPRs free.
   const int lrow = lane / S::kChunks;
   const int lpos = lane % S::kChunks;
-  auto issue = [&](int kt) {
-    uint8_t* buf = smem + (kt % STAGES) * kStage;
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(smem) + wave * kLoads * 1024);
+  auto issue = [&](int kl) {  // local stage index kl: K stage kt0 + kl, ring slot kl % STAGES
+    const int kt = kt0 + kl;
+    const uint32_t buf = lds_base + (kl % STAGES) * kStage;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int blk = wave * kLoads + i;
@@ -481,7 +519,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
       } else {
         p = A + min(m0 + (row - kBigBN), e.M - 1) * lda + k0;
       }
-      __builtin_amdgcn_global_load_lds((global_void_ptr)p, (lds_void_ptr)(buf + blk * 1024), 16, 0, 0);
+      dma16(p, buf + i * 1024);
     }
   };
 
@@ -502,7 +540,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
       v8i af[kFM];
 #pragma unroll
       for (int j = 0; j < kFM; ++j) {
-        const int row = kBigBN + wm * (BM / 2) + j * 32 + frow;
+        const int row = kBigBN + wm * 64 + j * 32 + frow;
         af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
 #pragma unroll
@@ -544,6 +582,36 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
     return;
   }
 #endif
+  if (part.base) {
+    // Split-K: store this slice's raw accumulators; splitk_reduce applies the
+    // epilogue. Through the same LDS transpose, 128 packed columns per row.
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    float* tile = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
+    const int64_t nw = n0 + wn * 128;
+    const int64_t mw = m0 + wm * 64;
+    const int col = (lane & 31) * 4;
+#pragma unroll
+    for (int j = 0; j < kFM; ++j) {
+#pragma unroll
+      for (int i = 0; i < kFN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (nw + col < e.N) {
+#pragma unroll 4
+        for (int r = lane >> 5; r < 32; r += 2) {
+          const int64_t m = mw + j * 32 + r;
+          if (m < e.M)
+            *reinterpret_cast<float4*>(part.base + (split * e.M + m) * part.ld + nw + col) =
+                *reinterpret_cast<const float4*>(tile + r * kPitch + col);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    return;
+  }
   // Epilogue through LDS, one 32-token fragment row at a time.
   // (1) Raw fp32 accumulators go to this wave's private [token][packed column]
   //     tile (row pitch padded by 16 bytes: the 16 rows written by 16 lanes
@@ -559,7 +627,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
   constexpr int kRowsPerPass = 64 / kLanesPerRow;
   constexpr int kRowIters = 32 / kRowsPerPass;
   const int64_t nw = n0 + wn * 128;                // first (packed) weight row of the wave tile
-  const int64_t mw = m0 + wm * (BM / 2);           // first token of the wave tile
+  const int64_t mw = m0 + wm * 64;                 // first token of the wave tile
   const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
   const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
   const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
@@ -605,7 +673,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
       const int r = r0 + t * kRowsPerPass;
       const int64_t m = mw + j * 32 + r;
       if (col_ok && m < e.M) {
-        const float sa = s_sa[wm * (BM / 2) + j * 32 + r];
+        const float sa = s_sa[wm * 64 + j * 32 + r];
         const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
         const float va[4] = {v.x, v.y, v.z, v.w};
         const float ra[4] = {res[t].x, res[t].y, res[t].z, res[t].w};
@@ -636,6 +704,30 @@ __global__ __launch_bounds__(256, OCC) void gemm_big(const uint8_t* __restrict__
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+}
+
+// Split-K finish: sums the K slices' partial accumulators in slice order
+// (deterministic) and applies the full epilogue. One thread per four output
+// columns of one token.
+template <bool GLU>
+__global__ __launch_bounds__(256) void splitk_reduce(Partials part, int ksplit, Epi e) {
+  const int64_t n_out = GLU ? e.N / 2 : e.N;
+  const int64_t groups = n_out / 4;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= e.M * groups) return;
+  const int64_t m = idx / groups;
+  const int64_t c = (idx - m * groups) * 4;                 // output column
+  const int64_t ng = GLU ? (c >> 4) * 32 + (c & 15) : c;   // packed row of its (gate) group
+  v4f a = v4f{0.f, 0.f, 0.f, 0.f}, u = a;
+  for (int s = 0; s < ksplit; ++s) {
+    const float* row = part.base + (s * e.M + m) * part.ld;
+    a += *reinterpret_cast<const v4f*>(row + ng);
+    if constexpr (GLU) u += *reinterpret_cast<const v4f*>(row + ng + 16);
+  }
+  float y[4];
+  if constexpr (GLU) epi_pre_glu(e, a, u, ng, m, y);
+  else epi_pre(e, a, ng, m, y);
+  epi_finish4(e, m, c, y);
 }
 
 // ---------------------------------------------------------------------------
@@ -821,15 +913,51 @@ int launch_lds(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
   return launch_status();
 }
 
+// Large-M launch plan: tiles and, when there are too few tiles to fill the
+// GPU, a K split (each slice at least 4 stages) finished by splitk_reduce.
+struct BigPlan {
+  int64_t tiles_m, tiles_n;
+  int ksplit;
+  int64_t kstages;  // K stages per slice
+  size_t ws_bytes;  // fp32 partials of all slices
+};
+
+__host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int kb) {
+  BigPlan p{};
+  p.tiles_m = (M + bm - 1) / bm;
+  p.tiles_n = (N + kBigBN - 1) / kBigBN;
+  const int64_t tiles = p.tiles_m * p.tiles_n;
+  const int64_t nk = K / kb;
+  int64_t s = 1;
+  if (tiles < 192) {
+    s = (320 + tiles - 1) / tiles;
+    if (s > nk / 4) s = nk / 4;
+    if (s < 1) s = 1;
+  }
+  p.kstages = (nk + s - 1) / s;
+  p.ksplit = static_cast<int>((nk + p.kstages - 1) / p.kstages);
+  p.ws_bytes = p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
+  return p;
+}
+
 template <int BM, int KB, int STAGES, int OCC, bool GLU>
 int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e,
-               hipStream_t st) {
-  const int64_t tiles_m = (e.M + BM - 1) / BM;
-  const int64_t tiles_n = (e.N + kBigBN - 1) / kBigBN;
-  if (tiles_m * tiles_n > 0x7FFFFFF0LL) return IFX_ERR_UNSUPPORTED;
-  const TileMap t = make_tile_map(tiles_m, tiles_n);
-  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(256), 0, st, a, lda, w,
-                     ldw, K, t, e);
+               void* ws, size_t ws_bytes, hipStream_t st) {
+  const BigPlan p = big_plan(e.M, e.N, K, BM, KB);
+  if (p.tiles_m * p.tiles_n * p.ksplit > 0x7FFFFFF0LL) return IFX_ERR_UNSUPPORTED;
+  Partials part{nullptr, e.N, p.kstages};
+  if (p.ksplit > 1) {
+    if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
+    part.base = static_cast<float*>(ws);
+  }
+  const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
+  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(2 * BM),
+                     0, st, a, lda, w, ldw, K, t, e, part);
+  if (p.ksplit > 1) {
+    const int64_t threads = e.M * ((GLU ? e.N / 2 : e.N) / 4);
+    hipLaunchKernelGGL((splitk_reduce<GLU>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, st,
+                       part, p.ksplit, e);
+  }
   return launch_status();
 }
 
@@ -862,18 +990,26 @@ int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint
 
 constexpr int64_t kSkinnyMaxM = 64;
 
-#ifndef IFX_BIG_BM
-#define IFX_BIG_BM 128
-#endif
-#ifndef IFX_BIG_STAGES
-#define IFX_BIG_STAGES 2
-#endif
-#ifndef IFX_BIG_KB
-#define IFX_BIG_KB 64
-#endif
-#ifndef IFX_BIG_OCC
-#define IFX_BIG_OCC 2
-#endif
+// Large-M configurations:
+//  * wide:   256 x 256 tiles, 8 waves, 128-byte K stages, 2-deep ring
+//            (128 KB LDS, one workgroup per CU) -- shapes with many tiles;
+//  * narrow: 256 x 128 tiles, 4 waves, 64-byte stages, 3-deep ring (74 KB LDS,
+//            two workgroups per CU) -- twice the tiles, so fewer K splits
+//            (less partial-sum traffic) when the output is small.
+// Both need K % 128 == 0.
+constexpr int kBigKB = 128;
+
+inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; }
+
+// The wide tile unless it leaves fewer than 192 tiles.
+inline bool use_wide(int64_t M, int64_t N) { return ((M + 255) / 256) * ((N + 255) / 256) >= 192; }
+
+template <bool GLU>
+int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e, void* ws,
+                 size_t ws_bytes, hipStream_t st) {
+  if (use_wide(e.M, e.N)) return launch_big<256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+  return launch_big<128, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+}
 
 }  // namespace
 }  // namespace ifx
@@ -883,10 +1019,9 @@ using namespace ifx;
 extern "C" {
 
 size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue) {
-  // No kernel variant of this build needs a workspace; the argument pair is
-  // part of the ABI so a split-K variant can use one without a signature change.
-  (void)M; (void)N; (void)K; (void)epilogue;
-  return 0;
+  (void)epilogue;
+  if (M <= 0 || N <= 0 || K <= 0 || !big_path(M, K)) return 0;
+  return use_wide(M, N) ? big_plan(M, N, K, 256, 128).ws_bytes : big_plan(M, N, K, 128, 64).ws_bytes;
 }
 
 int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
@@ -925,9 +1060,9 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
     (void)workspace; (void)ws_bytes;
     return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, st) : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, st);
   }
-  if (K % IFX_BIG_KB == 0 && M > 128)
-    return glu ? launch_big<IFX_BIG_BM, IFX_BIG_KB, IFX_BIG_STAGES, IFX_BIG_OCC, true>(A, lda, Wt, ldw, K, e, st)
-               : launch_big<IFX_BIG_BM, IFX_BIG_KB, IFX_BIG_STAGES, IFX_BIG_OCC, false>(A, lda, Wt, ldw, K, e, st);
+  if (big_path(M, K))
+    return glu ? launch_large<true>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
+               : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
 }

@@ -51,9 +51,12 @@ def test_abi_version_and_status_strings(lib):
 
 
 def test_workspace_queries(lib):
-    # no variant of this build needs a workspace
+    # enough output tiles (or M <= 64): no split-K, no workspace
     assert lib.ifx_fp8_linear_workspace_size(8192, 3072, 3072, 0) == 0
     assert lib.ifx_fp8_linear_workspace_size(16, 6144, 1536, 0) == 0
+    # 816 x 2048 has 32 tiles: split-K partials, fp32, a whole number of M x N slices
+    ws = lib.ifx_fp8_linear_workspace_size(816, 2048, 16384, 0)
+    assert ws > 0 and ws % (816 * 2048 * 4) == 0
     assert lib.ifx_quant_tensor_workspace_size(0) == 0
     assert lib.ifx_quant_tensor_workspace_size(8193) == 8
 

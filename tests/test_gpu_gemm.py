@@ -229,3 +229,16 @@ def test_workspace_reuse_across_shapes(gpu, oracle_mod):
         from instinctflash_amd.kernels import linear
         out = linear(qa, sa, fw, out_dtype=torch.float32)
         _assert_close(_f(out), _ref(oracle_mod, qa, sa, fw), f"seq {i}: {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K,act", [(816, 2048, 16384, None), (1024, 2560, 2048, None), (300, 1024, 4096, "swiglu"),
+                                       (1024, 2048, 11008, None), (257, 512, 2048, "gelu_tanh")])
+def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
+    # few output tiles: the large-M kernel splits K and a reduce kernel applies the epilogue
+    from instinctflash_amd import _lib
+    from instinctflash_amd.kernels import pack_glu
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, 0) > 0
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N, bias=True)
+    res = torch.randn((M, N // 2 if act == "swiglu" else N), generator=g).to(torch.bfloat16)
+    w = pack_glu(fw) if act == "swiglu" else fw
+    _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
