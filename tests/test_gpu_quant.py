@@ -278,3 +278,26 @@ def test_graph_replay_matches_eager(gpu, oracle_mod):
         torch.cuda.synchronize()
         assert torch.equal(s, se)
         assert torch.equal(q.view(torch.uint8), qe.view(torch.uint8))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_wide_range_stress(gpu, oracle_mod, seed):
+    # 64 rows x 65536 fp32 values spanning ~80 binades, random signs, exact zeros,
+    # values at and beside every E4M3 midpoint of the row's scale: the fast
+    # division/packing path must give the oracle's bytes everywhere.
+    rng = np.random.default_rng(seed)
+    R, K = 64, 65536
+    mag = np.exp2(rng.uniform(-60, 20, size=(R, K))).astype(np.float32)
+    x = (mag * rng.choice([-1.0, 1.0], size=(R, K))).astype(np.float32)
+    x[:, :64] = 0.0
+    amax = np.abs(x).max(axis=1)
+    s = (np.maximum(amax, np.float32(1e-12)) * (np.float32(1) / np.float32(448))).astype(np.float32)
+    pos = np.unique(oracle_mod.E4M3_VALUES[~np.isnan(oracle_mod.E4M3_VALUES)]).astype(np.float64)
+    pos = pos[pos > 0]
+    mids = ((pos[1:] + pos[:-1]) / 2)[:, None] * s[None, :].astype(np.float64)   # [n_mid, R]
+    n = mids.shape[0]
+    for k, eps in enumerate((0.0, 1.0, -1.0)):
+        v = (mids * (1 + eps * 2.0 ** -23)).astype(np.float32).T                    # [R, n_mid]
+        x[:, 64 + k * n:64 + (k + 1) * n] = np.minimum(v, amax[:, None])
+    _check_rows(torch.from_numpy(x).to(gpu), oracle_mod)
+    _check_rows(torch.from_numpy(x).to(torch.bfloat16).to(gpu), oracle_mod)
