@@ -62,6 +62,8 @@ extern "C" {
  *   y = residual[m,n] + y                            IFX_EPI_RESIDUAL
  *   out[m,n] = round(y)                              bf16, or f32 with IFX_EPI_OUT_F32
  * residual is bf16 unless IFX_EPI_RES_F32. out may alias residual (in-place update).
+ * IFX_EPI_SCALAR_SA / IFX_EPI_SCALAR_SW: sa / sw point to ONE f32 shared by all
+ * tokens / weight rows (per-tensor scales, reference runtime/torch_fp8_linear.py:75-78).
  */
 #define IFX_EPI_NONE 0
 #define IFX_EPI_BIAS 1
@@ -72,6 +74,8 @@ extern "C" {
 #define IFX_EPI_GATE 32
 #define IFX_EPI_OUT_F32 64
 #define IFX_EPI_RES_F32 128
+#define IFX_EPI_SCALAR_SA 256
+#define IFX_EPI_SCALAR_SW 512
 
 int ifx_abi_version(void);
 /* Host pointer to a static string describing a status code. */

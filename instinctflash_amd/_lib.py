@@ -38,6 +38,8 @@ EPI_RESIDUAL = 16
 EPI_GATE = 32
 EPI_OUT_F32 = 64
 EPI_RES_F32 = 128
+EPI_SCALAR_SA = 256
+EPI_SCALAR_SW = 512
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64

@@ -59,6 +59,20 @@ __device__ __forceinline__ float4 load_f4_or(const float* p, int64_t i, float df
   return *reinterpret_cast<const float4*>(p + i);
 }
 
+// Token scale sa[m] (one shared value with IFX_EPI_SCALAR_SA; 1 if absent).
+__device__ __forceinline__ float epi_sa(const Epi& e, int64_t m) {
+  return e.sa ? e.sa[(e.flags & IFX_EPI_SCALAR_SA) ? 0 : m] : 1.0f;
+}
+
+// Weight scales sw[n..n+3] (one shared value with IFX_EPI_SCALAR_SW; 1 if absent).
+__device__ __forceinline__ float4 epi_sw4(const Epi& e, int64_t n) {
+  if (e.sw && (e.flags & IFX_EPI_SCALAR_SW)) {
+    const float v = e.sw[0];
+    return make_float4(v, v, v, v);
+  }
+  return load_f4_or(e.sw, n, 1.0f);
+}
+
 // y (four consecutive output columns c..c+3 of row m, after activation) ->
 // gate, residual, store.
 __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, float* y) {
@@ -94,8 +108,8 @@ __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, 
 // First half of the epilogue for one lane's D fragment (weight rows n..n+3,
 // token m): dequantization scales, bias, GELU. Caller guarantees m < M, n < N.
 __device__ __forceinline__ void epi_pre(const Epi& e, const v4f acc, int64_t n, int64_t m, float* y) {
-  const float sa = e.sa ? e.sa[m] : 1.0f;
-  const float4 sw = load_f4_or(e.sw, n, 1.0f);
+  const float sa = epi_sa(e, m);
+  const float4 sw = epi_sw4(e, n);
   const float4 b = load_f4_or((e.flags & IFX_EPI_BIAS) ? e.bias : nullptr, n, 0.0f);
   y[0] = acc[0] * sa * sw.x + b.x;
   y[1] = acc[1] * sa * sw.y + b.y;
@@ -140,9 +154,9 @@ __device__ __forceinline__ void epi_store(const Epi& e, const v4f acc, int64_t n
 // is 16 packed rows later. Caller guarantees m < M, ng < N.
 __device__ __forceinline__ void epi_pre_glu(const Epi& e, const v4f accg, const v4f accu, int64_t ng,
                                             int64_t m, float* y) {
-  const float sa = e.sa ? e.sa[m] : 1.0f;
-  const float4 swg = load_f4_or(e.sw, ng, 1.0f);
-  const float4 swu = load_f4_or(e.sw, ng + 16, 1.0f);
+  const float sa = epi_sa(e, m);
+  const float4 swg = epi_sw4(e, ng);
+  const float4 swu = epi_sw4(e, ng + 16);
   const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
   const float4 bg = load_f4_or(bp, ng, 0.0f);
   const float4 bu = load_f4_or(bp, ng + 16, 0.0f);
@@ -634,13 +648,13 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
   const bool col_ok = c_out < (GLU ? e.N / 2 : e.N);
   const int64_t np = col_ok ? nw + pc : 0;         // packed weight row (any valid row if unused)
   const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
-  const float4 sw0 = load_f4_or(e.sw, np, 1.0f);
+  const float4 sw0 = epi_sw4(e, np);
   const float4 b0 = load_f4_or(bp, np, 0.0f);
-  const float4 sw1 = GLU ? load_f4_or(e.sw, np + 16, 1.0f) : sw0;
+  const float4 sw1 = GLU ? epi_sw4(e, np + 16) : sw0;
   const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
   uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
   if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
-  if (tid < BM) s_sa[tid] = e.sa ? e.sa[min(m0 + tid, e.M - 1)] : 1.0f;
+  if (tid < BM) s_sa[tid] = epi_sa(e, min(m0 + tid, e.M - 1));
   asm volatile("" ::: "memory");
   __syncthreads();
   const float swa[4] = {sw0.x, sw0.y, sw0.z, sw0.w}, ba[4] = {b0.x, b0.y, b0.z, b0.w};
@@ -800,11 +814,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const int64_t c_epi = NBW == 2 ? (nrow0 >> 5) * 16 + 4 * g : nrow0 + 4 * g;  // output column
   float sa_epi = 1.0f, sw_epi[NBW][4], b_epi[NBW][4], gate_epi[4] = {1.f, 1.f, 1.f, 1.f}, res_epi[4] = {0.f, 0.f, 0.f, 0.f};
   if (wave < MB) {
-    if (e.sa) sa_epi = e.sa[mc];
+    sa_epi = epi_sa(e, mc);
     const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
 #pragma unroll
     for (int b = 0; b < NBW; ++b) {
-      const float4 w4 = load_f4_or(e.sw, nrow0 + b * 16 + 4 * g, 1.0f);
+      const float4 w4 = epi_sw4(e, nrow0 + b * 16 + 4 * g);
       const float4 b4 = load_f4_or(bp, nrow0 + b * 16 + 4 * g, 0.0f);
       sw_epi[b][0] = w4.x; sw_epi[b][1] = w4.y; sw_epi[b][2] = w4.z; sw_epi[b][3] = w4.w;
       b_epi[b][0] = b4.x; b_epi[b][1] = b4.y; b_epi[b][2] = b4.z; b_epi[b][3] = b4.w;
@@ -838,12 +852,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
         const uint8_t* p = wrow[b] + s * kBK;
+#ifdef IFX_DBG_SK_NO_W
+        wf[u][b] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
+#else
         wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
+#endif
       }
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
         const uint8_t* p = arow[j] + s * kBK;
+#ifdef IFX_DBG_SK_NO_A
+        af[u][j] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
+#else
         af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
+#endif
       }
     }
 #pragma unroll
@@ -1029,7 +1051,8 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                    const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                    int64_t K, void* workspace, size_t ws_bytes, void* stream) {
   constexpr int kKnown = IFX_EPI_BIAS | IFX_EPI_GELU_TANH | IFX_EPI_GEGLU | IFX_EPI_SWIGLU |
-                         IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32;
+                         IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32 |
+                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW;
   if (epilogue & ~kKnown) return IFX_ERR_INVALID;
   const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
   if ((epilogue & IFX_EPI_GEGLU) && (epilogue & IFX_EPI_SWIGLU)) return IFX_ERR_INVALID;
@@ -1047,7 +1070,7 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
   }
   if (!aligned16(a) || !aligned16(w) || !aligned16(out) || lda % 16 != 0 || ldw % 16 != 0 || ldo % 8 != 0)
     return IFX_ERR_ALIGN;
-  if ((sw && !aligned16(sw)) || (bias && !aligned16(bias)) || (gate && (reinterpret_cast<uintptr_t>(gate) & 7u)))
+  if ((sw && !(epilogue & IFX_EPI_SCALAR_SW) && !aligned16(sw)) || (bias && !aligned16(bias)) || (gate && (reinterpret_cast<uintptr_t>(gate) & 7u)))
     return IFX_ERR_ALIGN;
 
   Epi e{sa, sw, bias, residual, ldr, static_cast<const uint16_t*>(gate), out, ldo, epilogue, M, N};

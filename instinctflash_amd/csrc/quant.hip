@@ -334,6 +334,61 @@ __global__ __launch_bounds__(kBlock) void tensor_pack(const uint16_t* x, int64_t
     q[i] = static_cast<uint8_t>(q1(bf16_bits_to_f32(x[i]), s));
 }
 
+// Vector forms (count % 8 == 0, 16-byte aligned x, 8-byte aligned q): each lane
+// handles 16-byte groups of 8 elements, kTensorChunk / 8 groups per block.
+__global__ __launch_bounds__(kBlock) void tensor_amax_partial_vec(const uint16_t* x, int64_t count,
+                                                                 uint32_t* partial) {
+  __shared__ uint32_t red[kBlock / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTensorChunk;
+  uint32_t amax = 0;
+#pragma unroll
+  for (int j = 0; j < kTensorChunk / 8 / kBlock; ++j) {
+    const int64_t i = base + (static_cast<int64_t>(j) * kBlock + threadIdx.x) * 8;
+    if (i < count) {
+      const uint4 r = *reinterpret_cast<const uint4*>(x + i);
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t lo = w[t] & 0x7FFFu, hi = (w[t] >> 16) & 0x7FFFu;
+        amax = amax > lo ? amax : lo;
+        amax = amax > hi ? amax : hi;
+      }
+    }
+  }
+  amax = team_max<kBlock>(amax, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = amax;
+}
+
+__global__ __launch_bounds__(kBlock) void tensor_pack_vec(const uint16_t* x, int64_t count,
+                                                         const uint32_t* partial, int64_t nparts, uint8_t* q,
+                                                         float* scale) {
+  __shared__ uint32_t red[kBlock / 64];
+  float s;
+  if (partial) {
+    uint32_t amax = 0;
+    for (int64_t i = threadIdx.x; i < nparts; i += kBlock) amax = amax > partial[i] ? amax : partial[i];
+    amax = team_max<kBlock>(amax, red);
+    s = scale_from_amax_bits(amax << 16);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+  } else {
+    s = *scale;
+  }
+  // The reciprocal form needs |x| / s <= 448 (true when s comes from this tensor's
+  // amax); a caller-fixed scale can overflow x * (1/s), so it keeps the division.
+  const bool fast = partial != nullptr && finite_scale(s);
+  const float r = 1.0f / s;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTensorChunk;
+#pragma unroll
+  for (int j = 0; j < kTensorChunk / 8 / kBlock; ++j) {
+    const int64_t i = base + (static_cast<int64_t>(j) * kBlock + threadIdx.x) * 8;
+    if (i < count) {
+      float v[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(x + i), v);
+      *reinterpret_cast<uint2*>(q + i) = fast ? pack8_fast(v, s, r) : pack8_exact(v, s);
+    }
+  }
+}
+
 // ---- dequant_rows / GLU weight repack --------------------------------------
 
 __global__ __launch_bounds__(kBlock) void dequant_rows_kernel(const uint16_t* x, int64_t ldx,
@@ -416,11 +471,18 @@ int ifx_quant_tensor_bf16(const void* x, int64_t count, void* q, float* scale, v
   if (nparts > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
   if (!partial || partial_bytes < ifx_quant_tensor_workspace_size(count)) return IFX_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(tensor_amax_partial, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st,
-                     static_cast<const uint16_t*>(x), count, static_cast<uint32_t*>(partial));
-  hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st,
-                     static_cast<const uint16_t*>(x), count,
-                     static_cast<const uint32_t*>(partial), nparts, static_cast<uint8_t*>(q), scale);
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  if (count % 8 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0) {
+    hipLaunchKernelGGL(tensor_amax_partial_vec, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st, xs, count,
+                       static_cast<uint32_t*>(partial));
+    hipLaunchKernelGGL(tensor_pack_vec, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st, xs, count,
+                       static_cast<const uint32_t*>(partial), nparts, static_cast<uint8_t*>(q), scale);
+  } else {
+    hipLaunchKernelGGL(tensor_amax_partial, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st, xs, count,
+                       static_cast<uint32_t*>(partial));
+    hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0, st, xs, count,
+                       static_cast<const uint32_t*>(partial), nparts, static_cast<uint8_t*>(q), scale);
+  }
   return launch_status();
 }
 
@@ -429,10 +491,15 @@ int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void*
   if (count == 0) return IFX_OK;
   const int64_t nparts = (count + kTensorChunk - 1) / kTensorChunk;
   if (nparts > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
-  hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), count,
-                     static_cast<const uint32_t*>(nullptr), nparts, static_cast<uint8_t*>(q),
-                     const_cast<float*>(scale));
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  if (count % 8 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0)
+    hipLaunchKernelGGL(tensor_pack_vec, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), xs, count, static_cast<const uint32_t*>(nullptr), nparts,
+                       static_cast<uint8_t*>(q), const_cast<float*>(scale));
+  else
+    hipLaunchKernelGGL(tensor_pack, dim3(static_cast<unsigned>(nparts)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), xs, count, static_cast<const uint32_t*>(nullptr), nparts,
+                       static_cast<uint8_t*>(q), const_cast<float*>(scale));
   return launch_status();
 }
 

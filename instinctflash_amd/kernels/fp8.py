@@ -201,8 +201,18 @@ def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scale
         raise ValueError(f"out has {Mo} rows, expected {M}")
     sw = None
     if use_scales:
-        _vec("a_scale", sa, M, device=a.device)
-        sw = _vec("w.scale", w.scale, N, device=a.device)
+        # per-token [M] / per-channel [N] scales, or one shared value each
+        # (per-tensor recipe, reference runtime/torch_fp8_linear.py:75-78)
+        if sa is not None and sa.numel() == 1 and M != 1:
+            _vec("a_scale", sa, 1, device=a.device)
+            flags |= _lib.EPI_SCALAR_SA
+        else:
+            _vec("a_scale", sa, M, device=a.device)
+        if w.scale.numel() == 1 and N != 1:
+            sw = _vec("w.scale", w.scale, 1, device=a.device)
+            flags |= _lib.EPI_SCALAR_SW
+        else:
+            sw = _vec("w.scale", w.scale, N, device=a.device)
     bias = None
     if use_scales and w.bias is not None:
         bias = _vec("w.bias", w.bias, N, device=a.device)
@@ -251,6 +261,9 @@ def linear(a: torch.Tensor, a_scale: torch.Tensor, w: Fp8Weight, out: torch.Tens
            act: str | None = None, residual: torch.Tensor | None = None,
            gate: torch.Tensor | None = None, out_dtype=torch.bfloat16) -> torch.Tensor:
     """Fused FP8 projection: out = epilogue(a @ w.w^T * a_scale[m] * w.scale[n]).
+
+    ``a_scale`` is [M] (per token) or [1] (per tensor); ``w.scale`` is [N]
+    (per channel) or [1] (per tensor).
 
     Epilogue order: + w.bias; act (``gelu_tanh``, or ``geglu``/``swiglu`` on a
     :func:`pack_glu` weight, halving the width); * gate[n] (adaLN gate); +

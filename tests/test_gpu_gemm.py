@@ -242,3 +242,48 @@ def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
     res = torch.randn((M, N // 2 if act == "swiglu" else N), generator=g).to(torch.bfloat16)
     w = pack_glu(fw) if act == "swiglu" else fw
     _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (200, 512, 1024), (1024, 2048, 2048)])
+def test_per_tensor_scales(gpu, oracle_mod, M, N, K):
+    # per-tensor activation and weight scales (reference runtime/torch_fp8_linear.py:75-78)
+    from instinctflash_amd.kernels import Fp8Weight, linear, quantize_tensor
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.01
+    qa, sa = quantize_tensor(x.to(gpu))
+    qw, sw = quantize_tensor(w.to(gpu))
+    fw = Fp8Weight(qw, sw, b.to(gpu))
+    o32 = linear(qa, sa, fw, out_dtype=torch.float32)
+    o16 = linear(qa, sa, fw)
+    ref = oracle_mod.ref_linear(_q(qa), np.full(M, _f(sa)[0], np.float32), _q(qw), np.full(N, _f(sw)[0], np.float32),
+                                bias=b.numpy())
+    _assert_close(_f(o32), ref, "per-tensor")
+    assert torch.equal(o16.view(torch.int16), o32.to(torch.bfloat16).view(torch.int16))
+
+
+def test_fp8_linear_module(gpu, oracle_mod):
+    # Gfx950FP8Linear mirrors ThorFP8Linear (runtime/torch_fp8_linear.py:10-79)
+    from instinctflash_amd.modules import Gfx950FP8Linear
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(1024, 512, dtype=torch.bfloat16).to(gpu)
+    mod = Gfx950FP8Linear(lin)
+    x = torch.randn((3, 7, 1024), device=gpu).to(torch.bfloat16)
+    y = mod(x)
+    assert y.shape == (3, 7, 512) and y.dtype == torch.bfloat16
+    # weight recipe: per-tensor, reciprocal scale, bit-exact
+    wq, ws = oracle_mod.quant_tensor(lin.weight.detach().cpu().view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(_q(mod.weight_fp8), wq) and _f(mod.weight_scale).view(np.uint32)[0] == ws.view(np.uint32)[0]
+    xq, xs = oracle_mod.quant_tensor(x.reshape(-1, 1024).cpu().view(torch.int16).numpy().view(np.uint16))
+    ref = oracle_mod.ref_linear(xq, np.full(21, xs[0], np.float32), wq, np.full(512, ws[0], np.float32),
+                                bias=lin.bias.detach().float().cpu().numpy())
+    d, cos = oracle_mod.parity_stats(_f(y.reshape(-1, 512)), ref)
+    assert cos >= TOL_COS and d <= TOL_MAXD + 2.0 ** -8 * np.abs(ref).max() / np.sqrt(np.mean(ref ** 2))
+    assert mod(x[:0]).shape == (0, 7, 512)
+    with pytest.raises(ValueError):
+        mod(x.float())
+    with pytest.raises(TypeError):
+        Gfx950FP8Linear(torch.nn.Sequential(lin))
+    with pytest.raises(ValueError):
+        Gfx950FP8Linear(torch.nn.Linear(1000, 512, dtype=torch.bfloat16).to(gpu))

@@ -125,3 +125,12 @@ def test_workload_accounting_matches_published_table():
     assert abs(mb(C1) - 4.688) < 0.01 and abs(mb(C2, 4) - 77.29) < 0.05
     assert abs(mb(C3) - 149.27) < 0.05 and abs(mb(C4) - 139.34) < 0.05 and abs(mb(C5) - 906.23) < 0.05
     assert abs(4 * (quant_bytes(16, 1536) + quant_bytes(16, 6144)) / 1e6 - 1.475) < 0.002
+
+
+def test_fp8_linear_module_refuses_cpu_and_non_linear():
+    from instinctflash_amd.modules import Gfx950FP8Linear
+    lin = torch.nn.Linear(32, 16, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        Gfx950FP8Linear(torch.nn.Sequential(lin))
+    with pytest.raises(ValueError, match="gfx950"):
+        Gfx950FP8Linear(lin)  # CPU weights, no gfx950 target
