@@ -163,6 +163,33 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                    const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                    int64_t K, void* workspace, size_t ws_bytes, void* stream);
 
+/* Activation scaling of ifx_quant_linear. */
+#define IFX_SCALE_ROW 0    /* one scale per token (row) */
+#define IFX_SCALE_TENSOR 1 /* one scale for the whole [M, K] activation */
+
+/*
+ * Quantize bf16 activations x [M, K] (row stride ldx elements, ldx % 8 == 0,
+ * 16-byte aligned) to E4M3 with the recipe of ifx_quant_rows (IFX_SCALE_ROW) or
+ * ifx_quant_tensor_bf16 (IFX_SCALE_TENSOR) into the workspace, then run
+ * ifx_fp8_linear on the result with the same weight / epilogue arguments: two
+ * launches, the output bit-identical to those two calls in sequence.
+ * IFX_SCALE_TENSOR needs ldx == K (else IFX_ERR_UNSUPPORTED).
+ * workspace: ifx_quant_linear_workspace_size(...) bytes, 256-byte aligned, no
+ * initialization; calls that may overlap must not share one.
+ * a_scale: NULL, or [M] f32 (IFX_SCALE_ROW) / [1] f32 (IFX_SCALE_TENSOR) that
+ * receives the activation scales. IFX_EPI_SCALAR_SA is rejected (the scale is
+ * computed here); IFX_EPI_SCALAR_SW is honoured.
+ * Replaces: the body of ThorFP8Linear.forward (runtime/torch_fp8_linear.py:
+ * 66-78: dynamic_pack_bf16_e4m3 + torch._scaled_mm with per-tensor scales) and
+ * the engines' producer-quant -> gemm pair (kernels/norm.py:150-176 row_quant
+ * feeding kernels/fp8.py:50-53 gemm).
+ */
+size_t ifx_quant_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode);
+int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw, const float* sw,
+                     const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
+                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
+                     size_t ws_bytes, void* stream);
+
 /*
  * Repack a gate|up weight (rows [0,F) gate, [F,2F) up; e4m3 [2F,K] + f32 scale
  * [2F] + optional f32 bias [2F]) into the interleaved layout the GLU epilogue

@@ -40,6 +40,8 @@ EPI_OUT_F32 = 64
 EPI_RES_F32 = 128
 EPI_SCALAR_SA = 256
 EPI_SCALAR_SW = 512
+SCALE_ROW = 0
+SCALE_TENSOR = 1
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -58,6 +60,9 @@ SIGNATURES = {
     "ifx_gated_act_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _INT, _P, _I64, _P, _P]),
     "ifx_dequant_rows": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P]),
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
+    "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
+    "ifx_quant_linear": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64, _I64,
+                                _P, _P, _SZ, _P]),
     "ifx_fp8_linear": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64,
                               _I64, _I64, _P, _SZ, _P]),
     "ifx_fp8_pack_glu": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P]),

@@ -777,7 +777,8 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   w = IFX_SK_WAVES;
   while (w * p.nbw * p.mb > 32) w /= 2;
 #else
-  while (w < 16 && ksteps > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
+  const int wmax = p.nbw * p.mb == 1 ? 16 : 8;  // 16 waves leave 128 VGPRs: one 16 x 16 block
+  while (w < wmax && ksteps > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
 #endif
   p.waves = w;
   return p;
@@ -993,9 +994,21 @@ void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const u
 template <int MB, int NBW>
 void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
                       const Epi& e, hipStream_t st) {
-  if (p.waves >= 16 && 16 * NBW * MB <= 32) launch_skinny_w<MB, NBW, 16>(p, a, lda, w, ldw, K, e, st);
-  else if (p.waves >= 8 && 8 * NBW * MB <= 32) launch_skinny_w<MB, NBW, 8>(p, a, lda, w, ldw, K, e, st);
-  else launch_skinny_w<MB, NBW, 4>(p, a, lda, w, ldw, K, e, st);
+  // 16 waves (128 VGPRs each) only for one 16 x 16 output block per workgroup:
+  // more blocks' fragments do not fit without spilling
+  if constexpr (NBW * MB == 1) {
+    if (p.waves >= 16) {
+      launch_skinny_w<MB, NBW, 16>(p, a, lda, w, ldw, K, e, st);
+      return;
+    }
+  }
+  if constexpr (8 * NBW * MB <= 32) {
+    if (p.waves >= 8) {
+      launch_skinny_w<MB, NBW, 8>(p, a, lda, w, ldw, K, e, st);
+      return;
+    }
+  }
+  launch_skinny_w<MB, NBW, 4>(p, a, lda, w, ldw, K, e, st);
 }
 
 template <int NBW>
@@ -1046,10 +1059,14 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
   return use_wide(M, N) ? big_plan(M, N, K, 256, 128).ws_bytes : big_plan(M, N, K, 128, 64).ws_bytes;
 }
 
-int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
-                   const float* sw, const float* bias, const void* residual, int64_t ldr,
-                   const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
-                   int64_t K, void* workspace, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks shared by ifx_fp8_linear and ifx_quant_linear (everything but the
+// activation operand); IFX_OK when the call may proceed.
+int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias, const void* residual, int64_t ldr,
+                 const void* gate, int epilogue, const void* out, int64_t ldo, int64_t M, int64_t N, int64_t K) {
   constexpr int kKnown = IFX_EPI_BIAS | IFX_EPI_GELU_TANH | IFX_EPI_GEGLU | IFX_EPI_SWIGLU |
                          IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32 |
                          IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW;
@@ -1060,18 +1077,54 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
   if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0) return IFX_ERR_INVALID;
   if (glu && N % 32 != 0) return IFX_ERR_INVALID;
   const int64_t n_out = glu ? N / 2 : N;
-  if (lda < K || ldw < K || ldo < n_out) return IFX_ERR_INVALID;
+  if (ldw < K || ldo < n_out) return IFX_ERR_INVALID;
   if (M == 0) return IFX_OK;
-  if (!a || !w || !out) return IFX_ERR_INVALID;
+  if (!w || !out) return IFX_ERR_INVALID;
   if ((epilogue & IFX_EPI_BIAS) && !bias) return IFX_ERR_INVALID;
   if ((epilogue & IFX_EPI_GATE) && !gate) return IFX_ERR_INVALID;
   if (epilogue & IFX_EPI_RESIDUAL) {
     if (!residual || ldr < n_out || ldr % 8 != 0 || !aligned16(residual)) return IFX_ERR_INVALID;
   }
-  if (!aligned16(a) || !aligned16(w) || !aligned16(out) || lda % 16 != 0 || ldw % 16 != 0 || ldo % 8 != 0)
+  if (!aligned16(w) || !aligned16(out) || ldw % 16 != 0 || ldo % 8 != 0) return IFX_ERR_ALIGN;
+  if ((sw && !(epilogue & IFX_EPI_SCALAR_SW) && !aligned16(sw)) || (bias && !aligned16(bias)) ||
+      (gate && (reinterpret_cast<uintptr_t>(gate) & 7u)))
     return IFX_ERR_ALIGN;
-  if ((sw && !(epilogue & IFX_EPI_SCALAR_SW) && !aligned16(sw)) || (bias && !aligned16(bias)) || (gate && (reinterpret_cast<uintptr_t>(gate) & 7u)))
-    return IFX_ERR_ALIGN;
+  return IFX_OK;
+}
+
+inline size_t round256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+// Workspace of ifx_quant_linear: e4m3 copy of x (row stride K),
+// per-token scales, per-tensor amax partials, then the GEMM's own workspace.
+struct QlWorkspace {
+  size_t q, scale, partial, gemm, total;
+};
+
+QlWorkspace ql_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode) {
+  QlWorkspace w{};
+  w.q = round256(static_cast<size_t>(M) * K);
+  w.scale = round256(static_cast<size_t>(M) * sizeof(float));
+  w.partial = scale_mode == IFX_SCALE_TENSOR ? round256(ifx_quant_tensor_workspace_size(M * K)) : 0;
+  w.gemm = ifx_fp8_linear_workspace_size(M, N, K, epilogue);
+  w.total = w.q + w.scale + w.partial + w.gemm;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
+                   const float* sw, const float* bias, const void* residual, int64_t ldr,
+                   const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
+                   int64_t K, void* workspace, size_t ws_bytes, void* stream) {
+  const int rc = check_linear(w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (lda < K) return IFX_ERR_INVALID;
+  if (M == 0) return IFX_OK;
+  if (!a) return IFX_ERR_INVALID;
+  if (!aligned16(a) || lda % 16 != 0) return IFX_ERR_ALIGN;
+  const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
 
   Epi e{sa, sw, bias, residual, ldr, static_cast<const uint16_t*>(gate), out, ldo, epilogue, M, N};
   const uint8_t* A = static_cast<const uint8_t*>(a);
@@ -1088,6 +1141,43 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
+}
+
+size_t ifx_quant_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return ql_workspace(M, N, K, epilogue, scale_mode).total;
+}
+
+int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw, const float* sw,
+                     const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
+                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
+                     size_t ws_bytes, void* stream) {
+  if (scale_mode != IFX_SCALE_ROW && scale_mode != IFX_SCALE_TENSOR) return IFX_ERR_INVALID;
+  if (epilogue & IFX_EPI_SCALAR_SA) return IFX_ERR_INVALID;  // the scale is computed here
+  const int rc = check_linear(w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (ldx < K) return IFX_ERR_INVALID;
+  if (M == 0) return IFX_OK;
+  if (!x) return IFX_ERR_INVALID;
+  if (!aligned16(x) || ldx % 8 != 0) return IFX_ERR_ALIGN;
+  // the stand-alone quantizer into the workspace, then the GEMM
+  const QlWorkspace ql = ql_workspace(M, N, K, epilogue, scale_mode);
+  if (!workspace || ws_bytes < ql.total || (reinterpret_cast<uintptr_t>(workspace) & 255u)) return IFX_ERR_WORKSPACE;
+  if (scale_mode == IFX_SCALE_TENSOR && ldx != K) return IFX_ERR_UNSUPPORTED;
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  uint8_t* q = base;
+  float* sa = a_scale ? a_scale : reinterpret_cast<float*>(base + ql.q);
+  void* partial = base + ql.q + ql.scale;
+  void* gws = base + ql.q + ql.scale + ql.partial;
+  int r;
+  if (scale_mode == IFX_SCALE_TENSOR)
+    r = ifx_quant_tensor_bf16(x, M * K, q, sa, partial, ql.partial, stream);
+  else
+    r = ifx_quant_rows(x, IFX_DTYPE_BF16, ldx, M, K, q, K, sa, stream);
+  if (r != IFX_OK) return r;
+  const int flags = epilogue | (scale_mode == IFX_SCALE_TENSOR ? IFX_EPI_SCALAR_SA : 0);
+  return ifx_fp8_linear(q, K, sa, w, ldw, sw, bias, residual, ldr, gate, flags, out, ldo, M, N, K, gws, ql.gemm,
+                        stream);
 }
 
 }  // extern "C"

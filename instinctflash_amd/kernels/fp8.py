@@ -4,11 +4,12 @@ with fused epilogue, on gfx950 HIP kernels.
 Public names mirror the reference module instinctflash/kernels/fp8.py
 (``E4M3``, ``FP8_MAX``, ``Fp8Weight``, ``quantize_weight``, ``gemm``) so an
 engine that imports them runs unchanged; ``quant_rows``, ``linear``,
-``pack_glu`` and ``quantize_tensor`` are the fused entry points of this build.
+``pack_glu``, ``quantize_tensor`` and ``quant_linear`` are the fused entry points of
+this build.
 
 Every call validates its tensors on the host and raises ``ValueError`` before
 anything is launched; kernels run on the current HIP stream and never allocate
-(the split-K workspace is a cached, caller-side buffer, zero-filled once).
+(the split-K / quantization workspace is a cached buffer per stream).
 """
 from __future__ import annotations
 
@@ -91,7 +92,8 @@ _WORKSPACES: dict = {}
 
 
 def _workspace(nbytes: int, device, stream: int):
-    """Zero-filled workspace per (device, stream); the kernels leave it zeroed."""
+    """Workspace per (device, stream), reused by every call on that stream
+    (calls on one stream are ordered; the kernels need no initial contents)."""
     if nbytes == 0:
         return None
     key = (device.index, stream)
@@ -179,11 +181,12 @@ def pack_tensor(x: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
 # GEMM
 # ---------------------------------------------------------------------------
 
-def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scales=True):
-    M, K, lda = _rows("a", a, E4M3)
-    N, Kw, ldw = _rows("w.w", w.w, E4M3, a.device)
+def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales):
+    """Validates the weight, output and epilogue operands of a projection of M
+    rows; returns (flags, N, ldw, sw, bias, ldr, ldo)."""
+    N, Kw, ldw = _rows("w.w", w.w, E4M3, device)
     if Kw != K:
-        raise ValueError(f"a has K={K} but the weight has K={Kw}")
+        raise ValueError(f"the activations have K={K} but the weight has K={Kw}")
     glu = bool(flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU))
     if glu and not w.glu:
         raise ValueError("GeGLU/SwiGLU epilogues need a weight repacked with pack_glu()")
@@ -196,26 +199,21 @@ def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scale
         flags |= _lib.EPI_OUT_F32
     elif out.dtype != torch.bfloat16:
         raise ValueError(f"out must be bf16 or fp32, got {out.dtype}")
-    Mo, _, ldo = _rows("out", out, out.dtype, a.device, cols=n_out)
+    Mo, _, ldo = _rows("out", out, out.dtype, device, cols=n_out)
     if Mo != M:
         raise ValueError(f"out has {Mo} rows, expected {M}")
     sw = None
     if use_scales:
-        # per-token [M] / per-channel [N] scales, or one shared value each
-        # (per-tensor recipe, reference runtime/torch_fp8_linear.py:75-78)
-        if sa is not None and sa.numel() == 1 and M != 1:
-            _vec("a_scale", sa, 1, device=a.device)
-            flags |= _lib.EPI_SCALAR_SA
-        else:
-            _vec("a_scale", sa, M, device=a.device)
+        # per-channel [N] scales or one shared value (per-tensor recipe,
+        # reference runtime/torch_fp8_linear.py:75-78)
         if w.scale.numel() == 1 and N != 1:
-            sw = _vec("w.scale", w.scale, 1, device=a.device)
+            sw = _vec("w.scale", w.scale, 1, device=device)
             flags |= _lib.EPI_SCALAR_SW
         else:
-            sw = _vec("w.scale", w.scale, N, device=a.device)
+            sw = _vec("w.scale", w.scale, N, device=device)
     bias = None
     if use_scales and w.bias is not None:
-        bias = _vec("w.bias", w.bias, N, device=a.device)
+        bias = _vec("w.bias", w.bias, N, device=device)
         flags |= _lib.EPI_BIAS
     ldr = 0
     if residual is not None:
@@ -223,20 +221,36 @@ def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scale
             flags |= _lib.EPI_RES_F32
         elif residual.dtype != torch.bfloat16:
             raise ValueError("residual must be bf16 or fp32")
-        Mr, _, ldr = _rows("residual", residual, residual.dtype, a.device, cols=n_out)
+        Mr, _, ldr = _rows("residual", residual, residual.dtype, device, cols=n_out)
         if Mr != M:
             raise ValueError("residual must have M rows")
         flags |= _lib.EPI_RESIDUAL
     if gate is not None:
-        _vec("gate", gate, n_out, dtype=torch.bfloat16, device=a.device)
+        _vec("gate", gate, n_out, dtype=torch.bfloat16, device=device)
         flags |= _lib.EPI_GATE
+    if M:
+        for name, t in (("w.w", w.w), ("out", out)):
+            if t.data_ptr() % 16:
+                raise ValueError(f"{name} must be 16-byte aligned")
+        if ldw % 16 or ldo % 8 or (residual is not None and (ldr % 8 or residual.data_ptr() % 16)):
+            raise ValueError("row strides must be multiples of 16 bytes (w) and 8 elements (out, residual)")
+    return flags, N, ldw, sw, bias, ldr, ldo
+
+
+def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scales=True):
+    M, K, lda = _rows("a", a, E4M3)
+    flags, N, ldw, sw, bias, ldr, ldo = _epilogue(M, K, a.device, w, out, flags, residual, gate, use_scales)
+    if use_scales:
+        # per-token [M] scales or one shared value
+        if sa is not None and sa.numel() == 1 and M != 1:
+            _vec("a_scale", sa, 1, device=a.device)
+            flags |= _lib.EPI_SCALAR_SA
+        else:
+            _vec("a_scale", sa, M, device=a.device)
     if M == 0:
         return out
-    for name, t in (("a", a), ("w.w", w.w), ("out", out)):
-        if t.data_ptr() % 16:
-            raise ValueError(f"{name} must be 16-byte aligned")
-    if lda % 16 or ldw % 16 or ldo % 8 or (residual is not None and (ldr % 8 or residual.data_ptr() % 16)):
-        raise ValueError("row strides must be multiples of 16 bytes (a, w) and 8 elements (out, residual)")
+    if a.data_ptr() % 16 or lda % 16:
+        raise ValueError("a must be 16-byte aligned with a row stride that is a multiple of 16 bytes")
     lib = _lib.load()
     stream = _stream(a.device)
     nbytes = lib.ifx_fp8_linear_workspace_size(M, N, K, flags)
@@ -277,6 +291,44 @@ def linear(a: torch.Tensor, a_scale: torch.Tensor, w: Fp8Weight, out: torch.Tens
         n_out = w.w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.w.shape[0]
         out = torch.empty((a.shape[0], n_out), dtype=out_dtype, device=a.device)
     return _linear(a, a_scale, w, out, flags, residual=residual, gate=gate)
+
+
+def quant_linear(x: torch.Tensor, w: Fp8Weight, out: torch.Tensor | None = None, *,
+                 act: str | None = None, residual: torch.Tensor | None = None,
+                 gate: torch.Tensor | None = None, out_dtype=torch.bfloat16, per_tensor: bool = False,
+                 a_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """Quantize bf16 activations ``x`` [M, K] to E4M3 (per token, or per tensor
+    with ``per_tensor=True``) and project: the result equals
+    ``linear(*quant_rows(x), w, ...)`` (or with ``quantize_tensor``'s scale) bit
+    for bit; the E4M3 copy lives in the per-stream workspace. ``a_scale`` ([M],
+    or [1] per tensor), if given, receives the scales.
+    Replaces the reference's producer-quant + gemm pairs and the body of
+    ThorFP8Linear.forward (runtime/torch_fp8_linear.py:66-78)."""
+    if act not in ACTIVATIONS:
+        raise ValueError(f"unknown activation {act!r}; expected one of {sorted(k for k in ACTIVATIONS if k)}")
+    M, K, ldx = _rows("x", x, torch.bfloat16)
+    flags = ACTIVATIONS[act]
+    if out is None:
+        n_out = w.w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.w.shape[0]
+        out = torch.empty((M, n_out), dtype=out_dtype, device=x.device)
+    flags, N, ldw, sw, bias, ldr, ldo = _epilogue(M, K, x.device, w, out, flags, residual, gate, True)
+    mode = _lib.SCALE_TENSOR if per_tensor else _lib.SCALE_ROW
+    if a_scale is not None:
+        _vec("a_scale", a_scale, 1 if per_tensor else M, device=x.device)
+    if M == 0:
+        return out
+    if x.data_ptr() % 16 or ldx % 8:
+        raise ValueError("x must be 16-byte aligned with a row stride that is a multiple of 8 elements")
+    if per_tensor and ldx != K:
+        raise ValueError("per-tensor quantization needs contiguous rows")
+    lib = _lib.load()
+    stream = _stream(x.device)
+    nbytes = lib.ifx_quant_linear_workspace_size(M, N, K, flags, mode)
+    ws = _workspace(nbytes, x.device, stream)
+    _lib.check(lib.ifx_quant_linear(_ptr(x), ldx, mode, _ptr(w.w), ldw, _ptr(sw), _ptr(bias), _ptr(residual), ldr,
+                                    _ptr(gate), flags, _ptr(out), ldo, M, N, K, _ptr(a_scale), _ptr(ws), nbytes,
+                                    stream), "ifx_quant_linear")
+    return out
 
 
 def pack_glu(w: Fp8Weight) -> Fp8Weight:

@@ -19,7 +19,7 @@ import torch
 from torch import nn
 
 from .backend import is_gfx950
-from .kernels.fp8 import E4M3, Fp8Weight, linear, quantize_tensor
+from .kernels.fp8 import E4M3, Fp8Weight, quant_linear, quantize_tensor
 
 
 class Gfx950FP8Linear(nn.Module):
@@ -64,7 +64,7 @@ class Gfx950FP8Linear(nn.Module):
         if x.numel() == 0:
             return x.new_empty(shape)
         rows = x.reshape(-1, self.in_features).contiguous()
-        packed, scale = quantize_tensor(rows)
         bias = None if self.bias is None else self.bias.float()
-        out = linear(packed, scale, Fp8Weight(self.weight_fp8, self.weight_scale, bias))
+        # dynamic per-tensor activation scale, then the GEMM
+        out = quant_linear(rows, Fp8Weight(self.weight_fp8, self.weight_scale, bias), per_tensor=True)
         return out.reshape(shape)

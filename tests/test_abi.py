@@ -57,6 +57,13 @@ def test_workspace_queries(lib):
     # 816 x 2048 has 32 tiles: split-K partials, fp32, a whole number of M x N slices
     ws = lib.ifx_fp8_linear_workspace_size(816, 2048, 16384, 0)
     assert ws > 0 and ws % (816 * 2048 * 4) == 0
+    # quantize-and-project: the e4m3 copy + scales (+ per-tensor partials) + the GEMM's own
+    assert lib.ifx_quant_linear_workspace_size(16, 6144, 1536, 0, _lib.SCALE_ROW) >= 16 * 1536 + 64
+    assert (lib.ifx_quant_linear_workspace_size(64, 6144, 1536, 0, _lib.SCALE_TENSOR)
+            > lib.ifx_quant_linear_workspace_size(64, 6144, 1536, 0, _lib.SCALE_ROW))
+    assert lib.ifx_quant_linear_workspace_size(100, 256, 512, 0, _lib.SCALE_ROW) >= 100 * 512 + 400
+    assert (lib.ifx_quant_linear_workspace_size(816, 2048, 16384, 0, _lib.SCALE_ROW)
+            >= 816 * 16384 + lib.ifx_fp8_linear_workspace_size(816, 2048, 16384, 0))
     assert lib.ifx_quant_tensor_workspace_size(0) == 0
     assert lib.ifx_quant_tensor_workspace_size(8193) == 8
 
@@ -93,6 +100,15 @@ def test_contract_violations_rejected_before_launch(lib):
     assert lib.ifx_gated_act_quant(fake, 64, 1, 32, None, None, 5, fake, 32, fake, None) == _lib.ERR_INVALID
     assert lib.ifx_quant_tensor_bf16(fake, 100, fake, fake, None, 0, None) == _lib.ERR_WORKSPACE
     assert lib.ifx_fp8_pack_glu(fake, fake, None, 24, 64, fake, fake, None, None) == _lib.ERR_INVALID
+    # quantize-and-project: bad scale mode, caller scalar scale, misaligned rows, no workspace
+    ql = lambda ldx, mode, epi, M, K, ws=None: lib.ifx_quant_linear(  # noqa: E731
+        fake, ldx, mode, fake, 64, fake, None, None, 0, None, epi, fake, 64, M, 64, K, None, ws, 0, None)
+    assert ql(64, 2, 0, 16, 64) == _lib.ERR_INVALID
+    assert ql(64, _lib.SCALE_ROW, _lib.EPI_SCALAR_SA, 16, 64) == _lib.ERR_INVALID
+    assert ql(60, _lib.SCALE_ROW, 0, 16, 48) == _lib.ERR_ALIGN
+    assert ql(64, _lib.SCALE_ROW, 0, 100, 64) == _lib.ERR_WORKSPACE
+    assert ql(64, _lib.SCALE_ROW, 0, 16, 64) == _lib.ERR_WORKSPACE
+    assert ql(64, _lib.SCALE_ROW, 0, 0, 64) == _lib.OK
     assert lib.ifx_dequant_rows(fake, 64, 1, 64, None, None, None, fake, 9, 64, None) == _lib.ERR_INVALID
 
 
