@@ -146,10 +146,13 @@ int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const flo
  * lda/ldw multiples of 16, ldo/ldr multiples of 8. sa: f32 [M] or NULL,
  * sw: f32 [N] or NULL, bias: f32 [N] or NULL, gate: bf16 [N_out] or NULL.
  * workspace: at least ifx_fp8_linear_workspace_size(M,N,K,epilogue) bytes of
- * 16-byte aligned device memory. It holds split-K partial sums (fp32) when the
- * output has too few 256 x 256 tiles to fill the GPU; the size is 0 (NULL
- * allowed) otherwise. No initialization is needed and nothing is kept between
- * calls; calls that may overlap must not share a workspace.
+ * 16-byte aligned device memory, used when the GEMM splits K across
+ * workgroups (too few output tiles, or for M <= 64 too few 16-row groups, to
+ * fill the GPU); the size is 0 (NULL allowed) otherwise. Layout: a 1 KB header
+ * of per-group arrival counters, then fp32 partial sums. Zero-fill a workspace
+ * once before its first use; every call leaves the header zeroed again, so one
+ * workspace serves any sequence of calls and shapes. Calls that may overlap
+ * must not share a workspace.
  * With sa = sw = NULL and epilogue 0 this is the raw-accumulator GEMM of
  * instinctflash/kernels/fp8.py:50-53 `gemm` (torch._scaled_mm with unit scales,
  * bf16 out). With scales and flags it fuses the consumers
@@ -174,8 +177,9 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
  * ifx_fp8_linear on the result with the same weight / epilogue arguments: two
  * launches, the output bit-identical to those two calls in sequence.
  * IFX_SCALE_TENSOR needs ldx == K (else IFX_ERR_UNSUPPORTED).
- * workspace: ifx_quant_linear_workspace_size(...) bytes, 256-byte aligned, no
- * initialization; calls that may overlap must not share one.
+ * workspace: ifx_quant_linear_workspace_size(...) bytes, 256-byte aligned,
+ * zero-filled once before first use like ifx_fp8_linear's (its header comes
+ * first); calls that may overlap must not share one.
  * a_scale: NULL, or [M] f32 (IFX_SCALE_ROW) / [1] f32 (IFX_SCALE_TENSOR) that
  * receives the activation scales. IFX_EPI_SCALAR_SA is rejected (the scale is
  * computed here); IFX_EPI_SCALAR_SW is honoured.

@@ -31,6 +31,8 @@
 //    fragments straight from HBM into MFMA registers (no LDS staging), and their
 //    partial sums are added in LDS in a fixed order (deterministic).
 
+#include <algorithm>
+
 #include "ifx_abi.h"
 #include "ifx_device.h"
 
@@ -748,20 +750,40 @@ __global__ __launch_bounds__(256) void splitk_reduce(Partials part, int ksplit, 
 // Skinny kernel (M <= 64): weight streaming
 // ---------------------------------------------------------------------------
 //
-// One workgroup owns 16 weight rows (32 for GLU: a gate block and its up block)
-// for the whole of K; its WAVES waves split K between them (wave w takes 128-byte
-// K steps w, w+WAVES, ...), each loading kSkUnroll steps of weight fragments
+// A group of 16 weight rows (32 for GLU: a gate block and its up block) is
+// split along K into ksplit slices, one workgroup per (group, slice), so that
+// shapes with few row groups still spread their bytes over every CU (a CU's
+// memory concurrency, not HBM, bounds a skinny GEMM that leaves CUs idle).
+// Inside a workgroup the WAVES waves split the slice's K steps (wave w takes
+// steps w, w+WAVES, ...), each loading kSkUnroll steps of weight fragments
 // (nontemporal: read once per call) and token fragments before issuing their
-// MFMAs, and the partial sums are added in LDS in wave order. No workgroup
-// waits for another, so the kernel needs no device-scope fences or workspace.
+// MFMAs; partial sums are added in LDS in wave order.
+//
+// With ksplit > 1 each workgroup stores its fp32 partial with agent-scope
+// (cross-XCD coherent) stores, waits for them to complete and takes a ticket
+// on its group's counter; the workgroup that takes the last ticket adds the
+// slices' partials in slice order (deterministic), resets the counter to zero
+// and runs the epilogue. No workgroup waits for another.
 
-constexpr int kSkUnroll = 4;  // K steps whose loads are issued together per wave
+constexpr int kSkUnroll = 4;       // K steps whose loads are issued together per wave
+constexpr int kSkMaxGroups = 256;  // row groups that may split K (one ticket each)
+constexpr size_t kWsHeader = kSkMaxGroups * sizeof(int);  // tickets at the workspace start
+
+struct SkSplit {
+  float* part;     // [ksplit][groups][NBW][MB][64 lanes] x 4 floats
+  int* tickets;    // [groups], zero between calls
+  int ksplit;
+  int64_t kss;     // K steps per slice
+};
 
 struct SkinnyPlan {
   int mb;          // 16-token blocks (1..4)
   int nbw;         // 16-row weight blocks per workgroup (1, or 2 for GLU)
-  int64_t groups;  // workgroups
+  int64_t groups;  // row groups
+  int ksplit;      // K slices per group (one workgroup each)
+  int64_t kss;     // K steps per slice
   int waves;       // waves per workgroup (4, 8 or 16)
+  size_t ws_bytes; // workspace (tickets + partials) when ksplit > 1
 };
 
 __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu) {
@@ -770,32 +792,63 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   p.nbw = glu ? 2 : 1;
   p.groups = N / (16 * p.nbw);
   const int64_t ksteps = (K + kBK - 1) / kBK;
-  // Enough waves that every wave has at most kSkUnroll K steps (one batch of
-  // loads in flight), within the LDS budget of the cross-wave reduction.
-  int w = 4;
-#ifdef IFX_SK_WAVES
-  w = IFX_SK_WAVES;
-  while (w * p.nbw * p.mb > 32) w /= 2;
+  // Split K in two when one token block meets at most 128 row groups (e.g. a
+  // 16 x 1536 x 6144 down projection: 96 groups would leave 160 CUs idle).
+  // Measured on MI355X: 9.4 -> 8.0 us there; more slices, or any split with
+  // several token blocks, lose more to the ticket and partial round trips
+  // (about 2-3 us of serial latency) than the extra CUs win.
+  int64_t s = 1;
+#ifdef IFX_SK_SPLIT
+  s = IFX_SK_SPLIT;
 #else
-  const int wmax = p.nbw * p.mb == 1 ? 16 : 8;  // 16 waves leave 128 VGPRs: one 16 x 16 block
-  while (w < wmax && ksteps > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
+  if (p.mb == 1 && p.groups <= kSkMaxGroups / 2 && ksteps >= 8) s = 2;
 #endif
+  if (s < 1 || p.groups > kSkMaxGroups) s = 1;
+  p.kss = (ksteps + s - 1) / s;
+  p.ksplit = static_cast<int>((ksteps + p.kss - 1) / p.kss);
+  // Enough waves that every wave has at most kSkUnroll K steps of its slice
+  // (one batch of loads in flight); 16 waves leave 128 VGPRs each, enough
+  // for one 16 x 16 block only.
+  int w = 4;
+  const int wmax = p.nbw * p.mb == 1 ? 16 : 8;
+  while (w < wmax && p.kss > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
   p.waves = w;
+  p.ws_bytes = p.ksplit > 1
+                   ? kWsHeader + static_cast<size_t>(p.ksplit) * p.groups * p.nbw * p.mb * 64 * 4 * sizeof(float)
+                   : 0;
   return p;
+}
+
+__device__ __forceinline__ void store_agent4(float* p, const v4f v) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) __hip_atomic_store(p + r, v[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ v4f load_agent4(const float* p) {
+  v4f v;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = __hip_atomic_load(p + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
 }
 
 template <int MB, int NBW, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
                                                           const uint8_t* __restrict__ W, int64_t ldw,
-                                                          int64_t K, Epi e) {
+                                                          int64_t K, Epi e, SkSplit sp) {
   __shared__ v4f red[WAVES][NBW][MB][64];
+  __shared__ int is_last;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t nrow0 = static_cast<int64_t>(blockIdx.x) * (16 * NBW);
+  const int64_t groups = e.N / (16 * NBW);
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) % groups;
+  const int slice = static_cast<int>(static_cast<int64_t>(blockIdx.x) / groups);
+  const int64_t nrow0 = grp * (16 * NBW);
   const int frow = lane & 15;
   const int g = lane >> 4;
   const int64_t ksteps = (K + kBK - 1) / kBK;
+  const int64_t s_begin = slice * sp.kss;
+  const int64_t s_end = min(s_begin + sp.kss, ksteps);
 
   const uint8_t* wrow[NBW];
 #pragma unroll
@@ -841,15 +894,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[b][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t s0 = wave; s0 < ksteps; s0 += WAVES * kSkUnroll) {
+  for (int64_t s0 = s_begin + wave; s0 < s_end; s0 += WAVES * kSkUnroll) {
     v8i wf[kSkUnroll][NBW];
     v8i af[kSkUnroll][MB];
 #pragma unroll
     for (int u = 0; u < kSkUnroll; ++u) {
       const int64_t s = s0 + u * WAVES;
       const int64_t k0 = s * kBK + g * 32;
-      const bool lo = s < ksteps && k0 < K;  // K % 16 == 0: a 16-byte half is all in or all out
-      const bool hi = s < ksteps && k0 + 16 < K;
+      const bool lo = s < s_end && k0 < K;  // K % 16 == 0: a 16-byte half is all in or all out
+      const bool hi = s < s_end && k0 + 16 < K;
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
         const uint8_t* p = wrow[b] + s * kBK;
@@ -883,40 +936,67 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #pragma unroll
     for (int j = 0; j < MB; ++j) red[wave][b][j][lane] = acc[b][j];
   __syncthreads();
-  // wave w finishes token block j = w (for w < MB) with the operands it
-  // prefetched before the K loop
+  // wave w finishes token block j = w (for w < MB)
+  const int j = wave;
+  v4f sum[NBW];
   if (wave < MB) {
-    const int j = wave;
-    v4f s[NBW];
 #pragma unroll
     for (int b = 0; b < NBW; ++b) {
-      s[b] = red[0][b][j][lane];
+      sum[b] = red[0][b][j][lane];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) s[b] += red[w][b][j][lane];
+      for (int w = 1; w < WAVES; ++w) sum[b] += red[w][b][j][lane];
     }
-    if (m_epi < e.M) {
-      float y[4];
-      if constexpr (NBW == 2) {
+  }
+
+  if (sp.ksplit > 1) {
+    // Publish this slice's partial; the last workgroup of the group adds them.
+    auto part = [&](int sl, int b) {
+      return sp.part + ((((static_cast<int64_t>(sl) * groups + grp) * NBW + b) * MB + j) * 64 + lane) * 4;
+    };
+    if (wave < MB) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float gv = s[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
-          const float uv = s[1][r] * sa_epi * sw_epi[1][r] + b_epi[1][r];
-          y[r] = ((e.flags & IFX_EPI_SWIGLU) ? silu(gv) : gelu_tanh(gv)) * uv;
-        }
-      } else {
+      for (int b = 0; b < NBW; ++b) store_agent4(part(slice, b), sum[b]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed before the ticket
+    __syncthreads();
+    if (tid == 0) {
+      const int t = __hip_atomic_fetch_add(sp.tickets + grp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = t == sp.ksplit - 1;
+      if (is_last) __hip_atomic_store(sp.tickets + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    if (wave < MB) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          y[r] = s[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
-          if (e.flags & IFX_EPI_GELU_TANH) y[r] = gelu_tanh(y[r]);
-        }
+      for (int b = 0; b < NBW; ++b) {
+        sum[b] = load_agent4(part(0, b));
+        for (int sl = 1; sl < sp.ksplit; ++sl) sum[b] += load_agent4(part(sl, b));
       }
+    }
+  }
+
+  if (wave < MB && m_epi < e.M) {
+    float y[4];
+    if constexpr (NBW == 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if (e.flags & IFX_EPI_GATE) y[r] = y[r] * gate_epi[r];
-        if (e.flags & IFX_EPI_RESIDUAL) y[r] = res_epi[r] + y[r];
+        const float gv = sum[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
+        const float uv = sum[1][r] * sa_epi * sw_epi[1][r] + b_epi[1][r];
+        y[r] = ((e.flags & IFX_EPI_SWIGLU) ? silu(gv) : gelu_tanh(gv)) * uv;
       }
-      epi_store4(e, m_epi, c_epi, y);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y[r] = sum[0][r] * sa_epi * sw_epi[0][r] + b_epi[0][r];
+        if (e.flags & IFX_EPI_GELU_TANH) y[r] = gelu_tanh(y[r]);
+      }
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (e.flags & IFX_EPI_GATE) y[r] = y[r] * gate_epi[r];
+      if (e.flags & IFX_EPI_RESIDUAL) y[r] = res_epi[r] + y[r];
+    }
+    epi_store4(e, m_epi, c_epi, y);
   }
 }
 
@@ -959,7 +1039,7 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int kb
   }
   p.kstages = (nk + s - 1) / s;
   p.ksplit = static_cast<int>((nk + p.kstages - 1) / p.kstages);
-  p.ws_bytes = p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
+  p.ws_bytes = p.ksplit > 1 ? kWsHeader + static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
   return p;
 }
 
@@ -971,7 +1051,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
   Partials part{nullptr, e.N, p.kstages};
   if (p.ksplit > 1) {
     if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
-    part.base = static_cast<float*>(ws);
+    part.base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);  // tickets stay untouched
   }
   const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
   hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(2 * BM),
@@ -986,39 +1066,45 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
 
 template <int MB, int NBW, int WAVES>
 void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                     const Epi& e, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES>), dim3(static_cast<unsigned>(p.groups)), dim3(WAVES * 64), 0,
-                     st, a, lda, w, ldw, K, e);
+                     const Epi& e, const SkSplit& sp, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES>), dim3(static_cast<unsigned>(p.groups * p.ksplit)),
+                     dim3(WAVES * 64), 0, st, a, lda, w, ldw, K, e, sp);
 }
 
 template <int MB, int NBW>
 void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                      const Epi& e, hipStream_t st) {
+                      const Epi& e, const SkSplit& sp, hipStream_t st) {
   // 16 waves (128 VGPRs each) only for one 16 x 16 output block per workgroup:
   // more blocks' fragments do not fit without spilling
   if constexpr (NBW * MB == 1) {
     if (p.waves >= 16) {
-      launch_skinny_w<MB, NBW, 16>(p, a, lda, w, ldw, K, e, st);
+      launch_skinny_w<MB, NBW, 16>(p, a, lda, w, ldw, K, e, sp, st);
       return;
     }
   }
   if constexpr (8 * NBW * MB <= 32) {
     if (p.waves >= 8) {
-      launch_skinny_w<MB, NBW, 8>(p, a, lda, w, ldw, K, e, st);
+      launch_skinny_w<MB, NBW, 8>(p, a, lda, w, ldw, K, e, sp, st);
       return;
     }
   }
-  launch_skinny_w<MB, NBW, 4>(p, a, lda, w, ldw, K, e, st);
+  launch_skinny_w<MB, NBW, 4>(p, a, lda, w, ldw, K, e, sp, st);
 }
 
 template <int NBW>
 int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                  const Epi& e, hipStream_t st) {
+                  const Epi& e, void* ws, size_t ws_bytes, hipStream_t st) {
+  SkSplit sp{nullptr, nullptr, p.ksplit, p.kss};
+  if (p.ksplit > 1) {
+    if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
+    sp.tickets = static_cast<int*>(ws);
+    sp.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);
+  }
   switch (p.mb) {
-    case 1: launch_skinny_mb<1, NBW>(p, a, lda, w, ldw, K, e, st); break;
-    case 2: launch_skinny_mb<2, NBW>(p, a, lda, w, ldw, K, e, st); break;
-    case 3: launch_skinny_mb<3, NBW>(p, a, lda, w, ldw, K, e, st); break;
-    default: launch_skinny_mb<4, NBW>(p, a, lda, w, ldw, K, e, st); break;
+    case 1: launch_skinny_mb<1, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
+    case 2: launch_skinny_mb<2, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
+    case 3: launch_skinny_mb<3, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
+    default: launch_skinny_mb<4, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
   }
   return launch_status();
 }
@@ -1054,8 +1140,9 @@ using namespace ifx;
 extern "C" {
 
 size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue) {
-  (void)epilogue;
-  if (M <= 0 || N <= 0 || K <= 0 || !big_path(M, K)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M <= kSkinnyMaxM) return skinny_plan(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0).ws_bytes;
+  if (!big_path(M, K)) return 0;
   return use_wide(M, N) ? big_plan(M, N, K, 256, 128).ws_bytes : big_plan(M, N, K, 128, 64).ws_bytes;
 }
 
@@ -1094,19 +1181,20 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
 
 inline size_t round256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
-// Workspace of ifx_quant_linear: e4m3 copy of x (row stride K),
-// per-token scales, per-tensor amax partials, then the GEMM's own workspace.
+// Workspace of ifx_quant_linear: the GEMM's own workspace first (its ticket
+// header must sit at offset 0 of every workspace), then the e4m3 copy of x
+// (row stride K), the per-token scales and the per-tensor amax partials.
 struct QlWorkspace {
-  size_t q, scale, partial, gemm, total;
+  size_t gemm, q, scale, partial, total;
 };
 
 QlWorkspace ql_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode) {
   QlWorkspace w{};
+  w.gemm = round256(std::max(ifx_fp8_linear_workspace_size(M, N, K, epilogue), kWsHeader));
   w.q = round256(static_cast<size_t>(M) * K);
   w.scale = round256(static_cast<size_t>(M) * sizeof(float));
   w.partial = scale_mode == IFX_SCALE_TENSOR ? round256(ifx_quant_tensor_workspace_size(M * K)) : 0;
-  w.gemm = ifx_fp8_linear_workspace_size(M, N, K, epilogue);
-  w.total = w.q + w.scale + w.partial + w.gemm;
+  w.total = w.gemm + w.q + w.scale + w.partial;
   return w;
 }
 
@@ -1133,8 +1221,8 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
 
   if (M <= kSkinnyMaxM) {
     const SkinnyPlan p = skinny_plan(M, N, K, glu);
-    (void)workspace; (void)ws_bytes;
-    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, st) : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, st);
+    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
+               : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   }
   if (big_path(M, K))
     return glu ? launch_large<true>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
@@ -1165,10 +1253,10 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
   if (!workspace || ws_bytes < ql.total || (reinterpret_cast<uintptr_t>(workspace) & 255u)) return IFX_ERR_WORKSPACE;
   if (scale_mode == IFX_SCALE_TENSOR && ldx != K) return IFX_ERR_UNSUPPORTED;
   uint8_t* base = static_cast<uint8_t*>(workspace);
-  uint8_t* q = base;
-  float* sa = a_scale ? a_scale : reinterpret_cast<float*>(base + ql.q);
-  void* partial = base + ql.q + ql.scale;
-  void* gws = base + ql.q + ql.scale + ql.partial;
+  void* gws = base;
+  uint8_t* q = base + ql.gemm;
+  float* sa = a_scale ? a_scale : reinterpret_cast<float*>(base + ql.gemm + ql.q);
+  void* partial = base + ql.gemm + ql.q + ql.scale;
   int r;
   if (scale_mode == IFX_SCALE_TENSOR)
     r = ifx_quant_tensor_bf16(x, M * K, q, sa, partial, ql.partial, stream);

@@ -93,7 +93,8 @@ _WORKSPACES: dict = {}
 
 def _workspace(nbytes: int, device, stream: int):
     """Workspace per (device, stream), reused by every call on that stream
-    (calls on one stream are ordered; the kernels need no initial contents)."""
+    (calls on one stream are ordered). Zero-filled when allocated: its header
+    holds the split-K arrival counters, which every call leaves at zero."""
     if nbytes == 0:
         return None
     key = (device.index, stream)

@@ -287,3 +287,30 @@ def test_fp8_linear_module(gpu, oracle_mod):
         Gfx950FP8Linear(torch.nn.Sequential(lin))
     with pytest.raises(ValueError):
         Gfx950FP8Linear(torch.nn.Linear(1000, 512, dtype=torch.bfloat16).to(gpu))
+
+
+@pytest.mark.parametrize("M,N,K,act", [(16, 1536, 6144, None), (1, 512, 1040, None), (9, 1024, 2064, "gelu_tanh"),
+                                       (16, 2048, 1536, "geglu"), (13, 4096, 16384, "swiglu")])
+def test_skinny_split_k(gpu, oracle_mod, M, N, K, act):
+    # one token block and <= 128 row groups: two workgroups per group split K and
+    # the last to arrive adds the partials (ticket counters in the workspace header)
+    from instinctflash_amd import _lib
+    from instinctflash_amd.kernels import fp8 as F, pack_glu
+    glu = act in ("geglu", "swiglu")
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) > 1024
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
+    n_out = N // 2 if glu else N
+    res = torch.randn((M, n_out), generator=g).to(torch.bfloat16)
+    w = pack_glu(fw) if glu else fw
+    o32, o16 = _check(gpu, oracle_mod, qa, sa, w, f"skinny split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+    # repeated calls: bit-identical (fixed slice order) and the counters return to zero
+    for _ in range(3):
+        again = F.linear(qa, sa, w, act=act, residual=res.to(gpu), out_dtype=torch.float32)
+        assert torch.equal(again.view(torch.int32), o32.view(torch.int32))
+    torch.cuda.synchronize()
+    for ws in F._WORKSPACES.values():
+        assert int(ws[:1024].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
+    # in place: out aliases the residual
+    r = res.to(gpu).clone()
+    F.linear(qa, sa, w, out=r, act=act, residual=r)
+    assert torch.equal(r.view(torch.int16), o16.view(torch.int16))
