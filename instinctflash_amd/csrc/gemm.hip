@@ -21,15 +21,19 @@
 // K permutation applied identically to both operands leaves the dot products
 // unchanged.
 //
-// Kernels
-//  * gemm_lds  (M > 64): BN x BM workgroup tile, BK = 128 bytes of K per stage,
-//    A and W tiles double-buffered in LDS (16-byte chunks XOR-swizzled by row so
-//    the fragment reads are bank-conflict free), global loads of stage k+1 in
-//    flight while stage k runs on the matrix cores, epilogue from registers.
-//  * gemm_skinny (M <= 64): bandwidth-bound on the weight stream. One workgroup
-//    owns 16 (32 for GLU) weight rows; its waves split K, stream weight
-//    fragments straight from HBM into MFMA registers (no LDS staging), and their
-//    partial sums are added in LDS in a fixed order (deterministic).
+// Kernels (dispatch in ifx_fp8_linear)
+//  * gemm_big (M > 128, K % 128 == 0): 256 weight rows x 256 (or 128) tokens
+//    per workgroup, 32x32x64 MFMAs, operands copied global -> LDS by
+//    direct-to-LDS DMA through a multi-stage ring, LDS-staged epilogue; split K
+//    (+ splitk_reduce) when the output has too few tiles to fill the GPU.
+//  * gemm_lds (M in 65..128, or K % 128 != 0): BN x BM tile, 16x16x128 MFMAs,
+//    register-staged double-buffered LDS tiles (16-byte chunks XOR-swizzled by
+//    row), epilogue from registers.
+//  * gemm_skinny (M <= 64): bound by the weight stream. A workgroup owns 16 (32
+//    for GLU) weight rows and a K slice; its waves split the slice, stream
+//    weight fragments straight from HBM into MFMA registers, and add their
+//    partial sums in LDS in a fixed order; slices of one row group are added
+//    by the last workgroup to arrive (deterministic, no waiting).
 
 #include <algorithm>
 
