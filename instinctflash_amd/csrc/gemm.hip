@@ -481,21 +481,22 @@ __device__ __forceinline__ v4f quad(const v16f& v, int q) {
   return v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
 }
 
-template <int BM, int KB, int STAGES, int OCC, bool GLU>
-__global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
+template <int BM, int KB, int STAGES, int OCC, bool GLU, int FM, bool PIPE>
+__global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
                                                      const uint8_t* __restrict__ W, int64_t ldw, int64_t K,
                                                      TileMap tmap, Epi e, Partials part) {
   using S = Swz<KB>;
   constexpr int kRows = kBigBN + BM;
   constexpr int kStage = kRows * KB;
   constexpr int kRowsPerDma = 1024 / KB;           // rows one DMA instruction fills
-  constexpr int kWM = BM / 64;                     // waves along tokens (2 along weight rows)
+  constexpr int kWT = 32 * FM;                     // tokens per wave tile
+  constexpr int kWM = BM / kWT;                    // waves along tokens (2 along weight rows)
   constexpr int kWaves = 2 * kWM;
   constexpr int kLoads = kRows / kRowsPerDma / kWaves;  // DMA instructions per wave per stage
   constexpr int kFN = 4;                           // 32-row weight fragments per wave (128 rows)
-  constexpr int kFM = 2;                           // 32-token fragments per wave (64 tokens)
+  constexpr int kFM = FM;                          // 32-token fragments per wave
   constexpr int kHalves = KB / 64;                 // 32x32x64 K steps per stage
-  static_assert(BM % 64 == 0 && kRows % (kWaves * kRowsPerDma) == 0, "tile");
+  static_assert(BM % kWT == 0 && kRows % (kWaves * kRowsPerDma) == 0, "tile");
   static_assert(KB == 64 || KB == 128, "stage depth");
   constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
   constexpr int kEpiBytes = kWaves * 32 * kPitch * 4;
@@ -508,7 +509,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wn = wave / kWM;  // weight-row half
-  const int wm = wave % kWM;  // 64-token slice
+  const int wm = wave % kWM;  // token slice of kWT tokens
 
   int tm, tn, split;
   if (!map_tile(tmap, tm, tn, split)) return;
@@ -560,7 +561,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
       v8i af[kFM];
 #pragma unroll
       for (int j = 0; j < kFM; ++j) {
-        const int row = kBigBN + wm * 64 + j * 32 + frow;
+        const int row = kBigBN + wm * kWT + j * 32 + frow;
         af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
 #pragma unroll
@@ -573,6 +574,68 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
     }
   };
 
+  if constexpr (PIPE) {
+    // Register-pipelined loop (KB = 64: one MFMA K step per stage). The
+    // fragments of stage kt+1 are read into the second register set right after
+    // the barrier that publishes stage kt+1, then the MFMAs of stage kt run on
+    // the first set, so LDS latency hides under matrix-core work even with one
+    // wave per SIMD. The DMA issued at iteration kt refills the slot of stage
+    // kt-1, whose fragments every wave consumed during iteration kt-1.
+    static_assert(KB == 64 && STAGES >= 3, "pipelined loop: 64-byte stages, >= 3-deep ring");
+    auto wait_stages = [&](int n) {  // at most n stages of this wave's DMA still in flight
+      if (n <= 0) wait_vmcnt<0>();
+      else if (n == 1) wait_vmcnt<kLoads>();
+      else if (n == 2) wait_vmcnt<2 * kLoads>();
+      else wait_vmcnt<3 * kLoads>();
+    };
+    const int c0 = 2 * fhalf;
+    auto load_frags = [&](const uint8_t* base, v8i (&wf)[kFN], v8i (&af)[kFM]) {
+#pragma unroll
+      for (int j = 0; j < kFM; ++j) {
+        const int row = kBigBN + wm * kWT + j * 32 + frow;
+        af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
+      }
+#pragma unroll
+      for (int i = 0; i < kFN; ++i) {
+        const int row = wn * 128 + i * 32 + frow;
+        wf[i] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
+      }
+    };
+    v8i wf[2][kFN], af[2][kFM];
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) issue(s);
+    wait_stages(min(STAGES - 2, nk - 1));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    load_frags(smem, wf[0], af[0]);
+    // two iterations per trip so the register sets alternate statically
+    for (int kt = 0; kt < nk; kt += 2) {
+#pragma unroll
+      for (int ph = 0; ph < 2; ++ph) {
+        const int t = kt + ph;
+        if (t < nk) {
+          if (t + 1 < nk) {
+            wait_stages(min(t + STAGES - 2, nk - 1) - (t + 1));
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+#ifndef IFX_DBG_NO_DMA
+            if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
+#endif
+            load_frags(smem + ((t + 1) % STAGES) * kStage, wf[ph ^ 1], af[ph ^ 1]);
+          }
+#ifndef IFX_DBG_NO_MFMA
+#pragma unroll
+          for (int i = 0; i < kFN; ++i)
+#pragma unroll
+            for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wf[ph][i], af[ph][j], acc[i][j]);
+#endif
+        }
+      }
+    }
+  } else {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nk) issue(s);
@@ -589,6 +652,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
 #ifndef IFX_DBG_NO_MFMA
     compute(smem + (kt % STAGES) * kStage);
 #endif
+  }
   }
 
 #ifdef IFX_DBG_NO_EPI
@@ -609,7 +673,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
     __syncthreads();
     float* tile = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
     const int64_t nw = n0 + wn * 128;
-    const int64_t mw = m0 + wm * 64;
+    const int64_t mw = m0 + wm * kWT;
     const int col = (lane & 31) * 4;
 #pragma unroll
     for (int j = 0; j < kFM; ++j) {
@@ -647,7 +711,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
   constexpr int kRowsPerPass = 64 / kLanesPerRow;
   constexpr int kRowIters = 32 / kRowsPerPass;
   const int64_t nw = n0 + wn * 128;                // first (packed) weight row of the wave tile
-  const int64_t mw = m0 + wm * 64;                 // first token of the wave tile
+  const int64_t mw = m0 + wm * kWT;                 // first token of the wave tile
   const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
   const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
   const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
@@ -660,7 +724,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
   const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
   uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
   if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
-  if (tid < BM) s_sa[tid] = epi_sa(e, min(m0 + tid, e.M - 1));
+  for (int t = tid; t < BM; t += kWaves * 64) s_sa[t] = epi_sa(e, min(m0 + t, e.M - 1));
   asm volatile("" ::: "memory");
   __syncthreads();
   const float swa[4] = {sw0.x, sw0.y, sw0.z, sw0.w}, ba[4] = {b0.x, b0.y, b0.z, b0.w};
@@ -693,7 +757,7 @@ __global__ __launch_bounds__(2 * BM, OCC) void gemm_big(const uint8_t* __restric
       const int r = r0 + t * kRowsPerPass;
       const int64_t m = mw + j * 32 + r;
       if (col_ok && m < e.M) {
-        const float sa = s_sa[wm * 64 + j * 32 + r];
+        const float sa = s_sa[wm * kWT + j * 32 + r];
         const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
         const float va[4] = {v.x, v.y, v.z, v.w};
         const float ra[4] = {res[t].x, res[t].y, res[t].z, res[t].w};
@@ -1047,7 +1111,7 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int kb
   return p;
 }
 
-template <int BM, int KB, int STAGES, int OCC, bool GLU>
+template <int BM, int KB, int STAGES, int OCC, bool GLU, int FM = 2, bool PIPE = false>
 int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e,
                void* ws, size_t ws_bytes, hipStream_t st) {
   const BigPlan p = big_plan(e.M, e.N, K, BM, KB);
@@ -1058,7 +1122,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
     part.base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);  // tickets stay untouched
   }
   const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
-  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(2 * BM),
+  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU, FM, PIPE>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
                      0, st, a, lda, w, ldw, K, t, e, part);
   if (p.ksplit > 1) {
     const int64_t threads = e.M * ((GLU ? e.N / 2 : e.N) / 4);
@@ -1132,6 +1196,11 @@ inline bool use_wide(int64_t M, int64_t N) { return ((M + 255) / 256) * ((N + 25
 template <bool GLU>
 int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e, void* ws,
                  size_t ws_bytes, hipStream_t st) {
+#ifdef IFX_EXP_BM
+  if (use_wide(e.M, e.N))
+    return launch_big<IFX_EXP_BM, IFX_EXP_KB, IFX_EXP_ST, IFX_EXP_OCC, GLU, IFX_EXP_FM, IFX_EXP_PIPE>(
+        a, lda, w, ldw, K, e, ws, ws_bytes, st);
+#endif
   if (use_wide(e.M, e.N)) return launch_big<256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   return launch_big<128, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
 }

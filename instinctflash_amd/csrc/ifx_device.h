@@ -40,8 +40,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two FP32 -> packed BF16 (lo in bits 0..15), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950 (NaN stays NaN).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // FP32 -> E4M3FN byte, round-to-nearest-even.
@@ -94,12 +99,15 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// GELU, tanh form: 0.5*x*(1+tanh(u)), u = sqrt(2/pi)*(x + 0.044715 x^3).
+// Since 0.5*(1+tanh(u)) = 1/(1+e^{-2u}), this is x / (1 + 2^z) with
+// z = -2u*log2(e) = x*(a + b*x^2): one FMA-based polynomial, one exp2 and one
+// reciprocal (hardware approximations, ~1 ulp each).
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715 x^3))), with tanh(u) = 1 - 2/(1+e^{2u}).
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // e^{2u}
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-  return 0.5f * x * (1.0f + t);
+  constexpr float a = -2.0 * 0.7978845608028654 * 1.4426950408889634;
+  constexpr float b = a * 0.044715;
+  const float z = x * __builtin_fmaf(b, x * x, a);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
 }
 
 __device__ __forceinline__ float silu(float x) {
