@@ -115,6 +115,25 @@ def summarize(wl, m):
     return res
 
 
+def probe(wl, dev, launches=20, copy_bytes=1 << 30):
+    """Counter-run helper: the dominant kernel alone, then a plain copy of known
+    size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
+    import torch
+    for _ in range(2):
+        wl.step()  # inputs of the dominant call, workspaces, code objects
+    torch.cuda.synchronize()
+    for i in range(launches):
+        wl.dominant_call(i)
+    torch.cuda.synchronize()
+    src = torch.empty(copy_bytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": wl.key, "dominant": wl.dominant, "launches": launches, "copy_bytes": copy_bytes}))
+
+
 def cpu_baseline(min_seconds=10.0):
     """Reference CPU FP8 path for one C2 unit (4 flow steps = 8 projections)."""
     import torch
@@ -146,6 +165,16 @@ def cpu_baseline(min_seconds=10.0):
             "cpu": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
 
+def measured_traffic(config):
+    """(bytes per launch, file) from profiles/hbm_traffic_<config>.md, if committed."""
+    import re
+    f = ROOT / "profiles" / f"hbm_traffic_{config}.md"
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", f.read_text())
+    return (int(m.group(1)), f"profiles/{f.name}") if m else None
+
+
 def _cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -164,6 +193,9 @@ def main():
     ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="launch only the dominant kernel (20x, no graph) and a 1 GiB device copy (20x), "
+                         "for rocprofv3 counter runs; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the FP8 projection path has no multi-GPU step in this build "
@@ -179,6 +211,9 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     arch = torch.cuda.get_device_properties(0).gcnArchName
+    if args.probe:
+        probe(CONFIGS[args.config](dev), dev)
+        return
 
     results = {}
     order = [args.config] + ([] if args.no_others else [k for k in CONFIGS if k != args.config])
@@ -207,6 +242,14 @@ def main():
                 "unit": "TFLOP/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = None
+    measured = measured_traffic(args.config)
+    if measured is not None:
+        # HBM bytes per launch of the dominant kernel from calibrated FETCH_SIZE /
+        # WRITE_SIZE counter runs (summary and commands in the profiles/ file)
+        roof["traffic"] = measured[0]
+        roof["traffic_source"] = measured[1]
+        roof["traffic_vs_algorithmic"] = round(measured[0] / d.bytes, 3)
+    roof["algorithmic_bytes"] = d.bytes
     roof["kernel"] = r["dominant"]["kernel"]
     roof["kernel_us"] = r["dominant"]["us"]
 

@@ -601,7 +601,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         wf[i] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
     };
-    v8i wf[2][kFN], af[2][kFM];
+    v8i wa[kFN], aa[kFM], wb[kFN], ab[kFM];  // two fragment register sets
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
       if (s < nk) issue(s);
@@ -609,32 +609,35 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    load_frags(smem, wf[0], af[0]);
-    // two iterations per trip so the register sets alternate statically
-    for (int kt = 0; kt < nk; kt += 2) {
-#pragma unroll
-      for (int ph = 0; ph < 2; ++ph) {
-        const int t = kt + ph;
-        if (t < nk) {
-          if (t + 1 < nk) {
-            wait_stages(min(t + STAGES - 2, nk - 1) - (t + 1));
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
+    load_frags(smem, wa, aa);
+    // publish stage t+1, refill the ring, read stage t+1 into the other set
+    auto advance = [&](int t, v8i (&wn_)[kFN], v8i (&an_)[kFM]) {
+      wait_stages(min(t + STAGES - 2, nk - 1) - (t + 1));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
 #ifndef IFX_DBG_NO_DMA
-            if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
+      if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
 #endif
-            load_frags(smem + ((t + 1) % STAGES) * kStage, wf[ph ^ 1], af[ph ^ 1]);
-          }
+      load_frags(smem + ((t + 1) % STAGES) * kStage, wn_, an_);
+    };
+    auto mfmas = [&](const v8i (&wc)[kFN], const v8i (&ac)[kFM]) {
 #ifndef IFX_DBG_NO_MFMA
 #pragma unroll
-          for (int i = 0; i < kFN; ++i)
+      for (int i = 0; i < kFN; ++i)
 #pragma unroll
-            for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wf[ph][i], af[ph][j], acc[i][j]);
+        for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wc[i], ac[j], acc[i][j]);
 #endif
-        }
-      }
+    };
+    // two stages per trip so the register sets alternate statically
+    int kt = 0;
+    for (; kt + 2 <= nk; kt += 2) {
+      if (kt + 1 < nk) advance(kt, wb, ab);
+      mfmas(wa, aa);
+      if (kt + 2 < nk) advance(kt + 1, wa, aa);
+      mfmas(wb, ab);
     }
+    if (kt < nk) mfmas(wa, aa);  // odd stage count: the last stage is in set a
   } else {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
