@@ -115,6 +115,31 @@ def summarize(wl, m):
     return res
 
 
+def measure_producers(dev, launches=32):
+    """The pre-norm producer (residual update + LayerNorm + adaLN + per-token
+    quant) at the C5 and C2 shapes: µs per call (graph of back-to-back calls,
+    median of 5) and GB/s of algorithmic bytes against the 8 TB/s roofline."""
+    import torch
+    from instinctflash_amd.workloads import PRODUCERS, NormQuant
+    res = {}
+    for key, (M, D) in PRODUCERS.items():
+        p = NormQuant(dev, M, D)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            p.step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = capture(lambda i: p.step(), launches, side)
+        time_graph(g)
+        us = sorted(time_graph(g)[0] / launches * 1e3 for _ in range(5))[2]
+        gbs = p.bytes / us / 1e3
+        res[key] = {"kernel": p.title, "us": round(us, 3), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                    "bytes": p.bytes}
+        _log(f"[bench] producer {key}: {p.title}: {us:.2f} us, {gbs:.0f} GB/s")
+    return res
+
+
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -262,6 +287,8 @@ def main():
                    "timed_unit": "4 flow-matching steps" if wl.steps_per_unit > 1 else "one pass"},
         "roofline": roof,
     }
+    if not args.no_others:
+        out["producers"] = measure_producers(dev)
     if not args.no_cpu:
         _log("[bench] CPU baseline (reference CPU FP8 path, one C2 unit)")
         out["cpu_baseline"] = cpu_baseline()

@@ -166,6 +166,39 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                    const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                    int64_t K, void* workspace, size_t ws_bytes, void* stream);
 
+/* Flags of ifx_residual_norm_quant. */
+#define IFX_RNQ_WRITE_RES 1 /* store the updated residual (only with delta) */
+#define IFX_RNQ_LAYERNORM 2 /* mean-centred LayerNorm instead of RMS norm */
+
+/*
+ * Pre-norm producer, one pass per row of res [M, D] (res_dtype F32 or BF16,
+ * row stride ldres elements):
+ *   if delta:  x = res + (delta * delta_row[m] * delta_col + bias) * gate,
+ *              stored back to res in its dtype with IFX_RNQ_WRITE_RES (the
+ *              stored value is the one normalized), else x = res
+ *   y = x / sqrt(mean(x^2) + eps)                  (RMS), or with IFX_RNQ_LAYERNORM
+ *   y = (x - mean) / sqrt(mean((x - mean)^2) + eps)
+ *   y = y * weight + beta;  y = y * (1 + mod_scale) + mod_shift
+ *   q, q_scale = per-row E4M3 of y (recipe of ifx_quant_rows); y stored if y != NULL
+ * delta: [M, D] BF16 or F32 raw accumulator (NULL: no residual update).
+ * delta_row [M], delta_col/bias/weight/beta [D]: f32, each may be NULL.
+ * gate, mod_scale, mod_shift: f32 [D], or tables [n, D] whose row mod_index[m]
+ * (int32 [M]) is used when mod_index != NULL; mod_scale and mod_shift come
+ * together. q: e4m3 [M, ldq] (NULL: no quantization; q_scale [M] f32 then).
+ * D % 8 == 0, D <= 16384; res/delta/y 16-byte aligned with row strides that
+ * are multiples of 8 elements; vectors 16-byte aligned.
+ * Replaces: instinctflash/kernels/norm.py:97-123 `residual_norm_quant` (kernel
+ * :25-94), with this package's quantization recipe (1e-12 floor, reciprocal
+ * scale, IEEE division) instead of the Triton 1e-8 floor / 448/amax multiply.
+ * The MoE router option (norm.py:84-94) is not provided.
+ */
+int ifx_residual_norm_quant(void* res, int res_dtype, int64_t ldres, const void* delta, int delta_dtype,
+                            int64_t lddelta, const float* delta_row, const float* delta_col, const float* bias,
+                            const float* gate, const float* weight, const float* beta, const float* mod_scale,
+                            const float* mod_shift, const int32_t* mod_index, int flags, float eps, void* q,
+                            int64_t ldq, float* q_scale, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t D,
+                            void* stream);
+
 /* Activation scaling of ifx_quant_linear. */
 #define IFX_SCALE_ROW 0    /* one scale per token (row) */
 #define IFX_SCALE_TENSOR 1 /* one scale for the whole [M, K] activation */

@@ -1,8 +1,8 @@
 """Consumer-side row kernels of the reference's FP8 pipeline, on HIP.
 
-``row_quant`` and ``dequant_rows`` keep the reference signatures
-(instinctflash/kernels/norm.py:150 and :178) so an engine can call them
-unchanged. The quantization they perform follows the bit-exact recipe of
+``residual_norm_quant``, ``row_quant`` and ``dequant_rows`` keep the reference
+signatures (instinctflash/kernels/norm.py:97, :150 and :178) so an engine can
+call them unchanged. The quantization they perform follows the bit-exact recipe of
 ``quant_rows`` (scale floor 1e-12, scale = amax * fl32(1/448), IEEE division).
 ``num_warps`` / ``block`` are accepted for signature compatibility; the HIP
 kernels pick their own launch shape.
@@ -44,3 +44,81 @@ def dequant_rows(x, y, *, row=None, col=None, bias=None, block=None, num_warps=4
     dt = _lib.DTYPE_F32 if y.dtype == torch.float32 else _lib.DTYPE_BF16
     _lib.check(_lib.load().ifx_dequant_rows(_ptr(x), ldx, M, D, _ptr(row), _ptr(col), _ptr(bias), _ptr(y),
                                             dt, ldy, _stream(x.device)), "ifx_dequant_rows")
+
+
+def _table(name, t, D, rows_from_index, device):
+    """An f32 per-column vector [D], or with ``mod_index`` a contiguous [n, D] table."""
+    if t is None:
+        return None
+    if t.device != device or t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor on {device}")
+    if rows_from_index:
+        if t.numel() % D or t.numel() == 0:
+            raise ValueError(f"{name} must be a [n, {D}] table when mod_index is given")
+    elif t.numel() != D:
+        raise ValueError(f"{name} must have {D} elements")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+    return t
+
+
+def residual_norm_quant(res, *, delta=None, delta_row=None, delta_col=None, bias=None, gate=None,
+                        write_res=True, layernorm=False, weight=None, beta=None,
+                        mod_scale=None, mod_shift=None, q=None, q_scale=None, y=None, eps=1e-6,
+                        num_warps=None, router=None, mod_index=None):
+    """Pre-norm producer, one pass per row of ``res`` [M, D] (fp32, or bf16):
+
+        if delta:  res[m] += (delta[m] * delta_row[m] * delta_col + bias) * gate
+        y[m] = norm(res[m])                        RMS, or LayerNorm with layernorm=True
+        y[m] = y[m] * weight + beta
+        y[m] = y[m] * (1 + mod_scale) + mod_shift
+        q[m], q_scale[m] = per-row E4M3 of y[m];   y written when given
+
+    Reference: instinctflash/kernels/norm.py:97-123 (same keywords; ``gate``,
+    ``mod_scale`` and ``mod_shift`` are [D], or [n, D] tables indexed per row by
+    the int32 ``mod_index``). The quantization is this package's recipe
+    (1e-12 floor, scale = amax * fl32(1/448), IEEE division) rather than the
+    Triton kernel's 1e-8 floor and 448/amax multiply. ``num_warps`` is accepted
+    for signature compatibility. The MoE ``router`` option is not provided."""
+    if router is not None:
+        raise ValueError("residual_norm_quant: the MoE router option is not provided by the gfx950 FP8 path")
+    if res.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("res must be float32 or bfloat16")
+    M, D, ldres = _rows("res", res, res.dtype)
+    dev = res.device
+    lddelta = 0
+    if delta is not None:
+        if delta.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("delta must be bfloat16 or float32")
+        Md, _, lddelta = _rows("delta", delta, delta.dtype, dev, cols=D)
+        if Md != M:
+            raise ValueError("delta must have as many rows as res")
+    _vec("delta_row", delta_row, M, device=dev)
+    for name, t in (("delta_col", delta_col), ("bias", bias), ("weight", weight), ("beta", beta)):
+        _table(name, t, D, False, dev)
+    indexed = mod_index is not None
+    if indexed:
+        _vec("mod_index", mod_index, M, dtype=torch.int32, device=dev)
+    for name, t in (("gate", gate), ("mod_scale", mod_scale), ("mod_shift", mod_shift)):
+        _table(name, t, D, indexed, dev)
+    if (mod_scale is None) != (mod_shift is None):
+        raise ValueError("mod_scale and mod_shift come together")
+    ldq = 0
+    if q is not None:
+        Mq, _, ldq = _rows("q", q, E4M3, dev, cols=D)
+        if Mq != M or q_scale is None:
+            raise ValueError("q needs M rows and a q_scale vector")
+        _vec("q_scale", q_scale, M, device=dev)
+    ldy = 0
+    if y is not None:
+        if y.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("y must be float32 or bfloat16")
+        My, _, ldy = _rows("y", y, y.dtype, dev, cols=D)
+        if My != M:
+            raise ValueError("y must have as many rows as res")
+    dt = lambda t: _lib.DTYPE_F32 if t is not None and t.dtype == torch.float32 else _lib.DTYPE_BF16  # noqa: E731
+    flags = (_lib.RNQ_WRITE_RES if write_res else 0) | (_lib.RNQ_LAYERNORM if layernorm else 0)
+    _lib.check(_lib.load().ifx_residual_norm_quant(
+        _ptr(res), dt(res), ldres, _ptr(delta), dt(delta), lddelta, _ptr(delta_row), _ptr(delta_col), _ptr(bias),
+        _ptr(gate), _ptr(weight), _ptr(beta), _ptr(mod_scale), _ptr(mod_shift), _ptr(mod_index), flags, float(eps),
+        _ptr(q), ldq, _ptr(q_scale), _ptr(y), dt(y), ldy, M, D, _stream(dev)), "ifx_residual_norm_quant")

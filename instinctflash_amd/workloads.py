@@ -347,3 +347,39 @@ class C5(Workload):
 
 
 CONFIGS = {"C1": C1, "C2": C2, "C3": C3, "C4": C4, "C5": C5}
+
+
+# ---------------------------------------------------------------------------
+# Producer: pre-norm residual update + LayerNorm + adaLN + per-token quant
+# ---------------------------------------------------------------------------
+
+class NormQuant:
+    """``residual_norm_quant`` at a pre-norm site: res (fp32) += (delta (bf16) *
+    row * col + bias) * gate, LayerNorm with adaptive scale/shift, per-token E4M3.
+    Algorithmic bytes: res read + write (8 B), delta (2 B), q (1 B) per element;
+    the [D] vectors once; q_scale and delta_row per row."""
+
+    def __init__(self, dev, M, D, seed=0):
+        from .kernels import norm as N
+        self.N, self.M, self.D = N, M, D
+        g = _gen(seed)
+        f = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+        self.base = f(M, D)
+        self.t = dict(res=self.base.clone(), delta=f(M, D).to(torch.bfloat16), delta_row=f(M).abs(),
+                      delta_col=f(D).abs(), bias=f(D), gate=f(D).abs(), mod_scale=f(D) * 0.1, mod_shift=f(D) * 0.1)
+        self.q = torch.empty((M, D), dtype=F.E4M3, device=dev)
+        self.qs = torch.empty(M, dtype=torch.float32, device=dev)
+        self.title = f"residual_norm_quant {M}x{D} (fp32 res += gated bf16 delta, LayerNorm, adaLN, e4m3)"
+
+    @property
+    def bytes(self) -> int:
+        return 11 * self.M * self.D + 5 * 4 * self.D + 2 * 4 * self.M
+
+    def step(self, i=0):
+        self.N.residual_norm_quant(self.t["res"], delta=self.t["delta"], delta_row=self.t["delta_row"],
+                                   delta_col=self.t["delta_col"], bias=self.t["bias"], gate=self.t["gate"],
+                                   layernorm=True, mod_scale=self.t["mod_scale"], mod_shift=self.t["mod_shift"],
+                                   q=self.q, q_scale=self.qs)
+
+
+PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}

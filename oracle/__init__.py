@@ -17,6 +17,13 @@ Parts
     followed by the epilogue math of kernels/norm.py:45-58,135-144,161-175 and
     kernels/activation.py:26-40. Pinned by fp64 brute force, closed forms and
     torch's independent GELU/SiLU implementations.
+  * residual_norm: the pre-norm producer of kernels/norm.py:25-94 (residual
+    update in float32 in the reference's operation order, norm in float64).
+    Pinned in tests/test_oracle.py by the reference's own test expectation
+    (tests/test_gi_kernels.py:93-112: the update equals res + (delta*dr*dc +
+    b)*gate to 1e-4, and the rsqrt-normalized row), by closed forms (a constant
+    row normalizes to +-1 / 0, unit-RMS rows are fixed points of RMS norm) and by
+    torch.nn.functional.layer_norm / rms_norm.
 """
 from __future__ import annotations
 
@@ -194,3 +201,57 @@ def parity_stats(out: np.ndarray, ref: np.ndarray):
     den = float(np.linalg.norm(o) * np.linalg.norm(r))
     cos = float(np.dot(o, r) / den) if den else 1.0
     return d / rms, cos
+
+
+def residual_norm(res, delta=None, delta_row=None, delta_col=None, bias=None, gate=None, write_res=True,
+                  layernorm=False, weight=None, beta=None, mod_scale=None, mod_shift=None, mod_index=None,
+                  eps=1e-6, res_bf16=False):
+    """Pre-norm producer of instinctflash/kernels/norm.py:25-94, restated.
+
+    res: float32 [M, D] values (for res_bf16, the float32 widening of the bf16
+    input). Returns (res_out float32 [M, D], y float64 [M, D]):
+      * res_out: the residual update in float32, operation by operation in the
+        reference's order (norm.py:46-56): d = delta*row; d = d*col; d = d+bias;
+        d = d*gate; x = res + d -- every step one IEEE float32 rounding, so a
+        device kernel without contraction reproduces it bit for bit; with
+        res_bf16 and write_res the stored value is rounded to bf16 (RNE) and that
+        rounded value is normalized (norm.py:56-57);
+      * y: the normalization (norm.py:58-66) and affine / adaptive terms
+        (:67-74) in float64 from res_out (RMS: x * 1/sqrt(mean(x^2) + eps);
+        LayerNorm: (x - mean) * 1/sqrt(mean((x - mean)^2) + eps)).
+    gate / mod_scale / mod_shift are [D], or [n, D] tables indexed by mod_index.
+    """
+    f32 = np.float32
+    x = np.asarray(res, dtype=f32).copy()
+    M, D = x.shape
+
+    def rows_of(t):
+        t = np.asarray(t, dtype=f32)
+        if mod_index is None:
+            return np.broadcast_to(t.reshape(1, D), (M, D))
+        return t.reshape(-1, D)[np.asarray(mod_index, dtype=np.int64)]
+
+    if delta is not None:
+        d = np.asarray(delta, dtype=f32).copy()
+        if delta_row is not None:
+            d = (d * np.asarray(delta_row, dtype=f32)[:, None]).astype(f32)
+        if delta_col is not None:
+            d = (d * np.asarray(delta_col, dtype=f32)[None, :]).astype(f32)
+        if bias is not None:
+            d = (d + np.asarray(bias, dtype=f32)[None, :]).astype(f32)
+        if gate is not None:
+            d = (d * rows_of(gate)).astype(f32)
+        x = (x + d).astype(f32)
+        if res_bf16 and write_res:
+            x = bf16_to_f32(f32_to_bf16(x))
+    xd = x.astype(np.float64)
+    if layernorm:
+        xd = xd - xd.mean(axis=1, keepdims=True)
+    y = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + float(f32(eps)))
+    if weight is not None:
+        y = y * np.asarray(weight, dtype=np.float64)[None, :]
+    if beta is not None:
+        y = y + np.asarray(beta, dtype=np.float64)[None, :]
+    if mod_scale is not None:
+        y = y * (1.0 + rows_of(mod_scale).astype(np.float64)) + rows_of(mod_shift).astype(np.float64)
+    return x, y

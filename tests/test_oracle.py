@@ -276,3 +276,79 @@ def test_golden_gemm(golden):
 def test_f32_to_bf16_rounding_matches_torch():
     x = np.random.default_rng(3).standard_normal(100000).astype(np.float32) * 1000
     assert np.array_equal(oracle.f32_to_bf16(x), bits(torch.from_numpy(x).to(torch.bfloat16)))
+
+
+# ---------------------------------------------------------------------------
+# residual_norm (kernels/norm.py:25-94)
+# ---------------------------------------------------------------------------
+
+def _rnq_inputs(M=33, D=1152, seed=3):
+    # the reference's own test case (tests/test_gi_kernels.py:93-112), on the CPU
+    g = torch.Generator().manual_seed(seed)
+    res = torch.randn(M, D, generator=g)
+    delta = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    dr, dc, b, gate = torch.rand(M, generator=g), torch.rand(D, generator=g), torch.randn(D, generator=g), \
+        torch.rand(D, generator=g)
+    w, beta = torch.rand(D, generator=g), torch.randn(D, generator=g)
+    ms, mh = torch.randn(D, generator=g) * 0.1, torch.randn(D, generator=g) * 0.1
+    return res, delta, dr, dc, b, gate, w, beta, ms, mh
+
+
+@pytest.mark.parametrize("layernorm", [False, True])
+def test_residual_norm_matches_reference_test_expectation(oracle_mod, layernorm):
+    res, delta, dr, dc, b, gate, w, beta, ms, mh = _rnq_inputs()
+    x, y = oracle_mod.residual_norm(res.numpy(), delta.float().numpy(), dr.numpy(), dc.numpy(), b.numpy(),
+                                    gate.numpy(), layernorm=layernorm, weight=w.numpy(), beta=beta.numpy(),
+                                    mod_scale=ms.numpy(), mod_shift=mh.numpy())
+    # the reference test's expectation, evaluated by torch in float32, op by op
+    expect = res + (delta.float() * dr[:, None] * dc + b) * gate
+    assert np.array_equal(x, expect.numpy())
+    xc = expect - expect.mean(-1, keepdim=True) if layernorm else expect
+    ty = xc * torch.rsqrt(xc.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ty = (ty * w + beta) * (1 + ms) + mh
+    assert np.abs(y - ty.double().numpy()).max() < 2e-5 * np.abs(y).max()
+
+
+def test_residual_norm_against_torch_norms(oracle_mod):
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(7, 640, generator=g) * 3 + 0.5
+    w, b = torch.rand(640, generator=g), torch.randn(640, generator=g)
+    _, y = oracle_mod.residual_norm(x.numpy(), layernorm=True, weight=w.numpy(), beta=b.numpy(), eps=1e-5)
+    ref = torch.nn.functional.layer_norm(x.double(), (640,), w.double(), b.double(), eps=float(np.float32(1e-5)))
+    assert np.abs(y - ref.numpy()).max() < 1e-12
+    _, y = oracle_mod.residual_norm(x.numpy(), weight=w.numpy(), eps=1e-6)
+    ref = torch.nn.functional.rms_norm(x.double(), (640,), w.double(), eps=float(np.float32(1e-6)))
+    assert np.abs(y - ref.numpy()).max() < 1e-12
+
+
+def test_residual_norm_closed_forms(oracle_mod):
+    D = 256
+    c = np.array([[2.0], [-0.5], [0.0]], dtype=np.float32) * np.ones((3, D), np.float32)
+    with np.errstate(invalid="ignore"):
+        _, y = oracle_mod.residual_norm(c, eps=0.0)
+    assert np.allclose(y[0], 1.0) and np.allclose(y[1], -1.0) and np.isnan(y[2]).all()  # 0/sqrt(0)
+    _, y = oracle_mod.residual_norm(c, layernorm=True, eps=1e-6)
+    assert np.abs(y).max() == 0.0  # constant rows centre to zero
+    # unit-RMS rows are fixed points of RMS norm (eps 0)
+    g = np.random.default_rng(0).standard_normal((4, D)).astype(np.float32)
+    g /= np.sqrt((g.astype(np.float64) ** 2).mean(axis=1, keepdims=True)).astype(np.float32)
+    _, y = oracle_mod.residual_norm(g, eps=0.0)
+    assert np.abs(y - g).max() < 1e-6
+
+
+def test_residual_norm_tables_and_bf16_store(oracle_mod):
+    rng = np.random.default_rng(1)
+    M, D, n = 6, 64, 3
+    res = rng.standard_normal((M, D)).astype(np.float32)
+    delta = rng.standard_normal((M, D)).astype(np.float32)
+    gate = rng.random((n, D)).astype(np.float32)
+    ms, mh = rng.standard_normal((n, D)).astype(np.float32), rng.standard_normal((n, D)).astype(np.float32)
+    idx = np.array([2, 0, 1, 1, 2, 0], dtype=np.int32)
+    x, y = oracle_mod.residual_norm(res, delta, gate=gate, mod_scale=ms, mod_shift=mh, mod_index=idx)
+    for m in range(M):  # row m uses table row idx[m]
+        xm, ym = oracle_mod.residual_norm(res[m:m + 1], delta[m:m + 1], gate=gate[idx[m]], mod_scale=ms[idx[m]],
+                                          mod_shift=mh[idx[m]])
+        assert np.array_equal(x[m], xm[0]) and np.array_equal(y[m], ym[0])
+    # bf16 residual: the stored (rounded) sum is what gets normalized
+    xb, _ = oracle_mod.residual_norm(res, delta, res_bf16=True)
+    assert np.array_equal(xb, oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16((res + delta).astype(np.float32))))
