@@ -76,6 +76,9 @@ extern "C" {
 #define IFX_EPI_RES_F32 128
 #define IFX_EPI_SCALAR_SA 256
 #define IFX_EPI_SCALAR_SW 512
+/* w is in the skinny tile layout written by ifx_fp8_pack_skinny (M <= 64 only;
+ * ldw is ignored). Not an epilogue option, but carried in the same flags. */
+#define IFX_EPI_W_TILED 1024
 
 int ifx_abi_version(void);
 /* Host pointer to a static string describing a status code. */
@@ -226,6 +229,21 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
                      const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
                      void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
                      size_t ws_bytes, void* stream);
+
+/*
+ * Repack an e4m3 weight [N, K] (row stride ldw; N % 16 == 0, K % 16 == 0) into
+ * the skinny tile layout read by ifx_fp8_linear with IFX_EPI_W_TILED: for each
+ * block of 16 rows b and each 128-byte K step s, one contiguous 2 KB tile
+ * T[b * ks + s] (ks = ceil(K / 128)); lane l (0..63) of the matrix-core
+ * fragment finds its 32 K bytes [32*(l/16), +32) of row 16b + l%16 at tile
+ * bytes [16l, 16l+16) and [1024+16l, +16), so every load instruction of the
+ * M <= 64 kernel reads 1 KB of contiguous memory. K is zero-padded to 128 * ks.
+ * Apply after ifx_fp8_pack_glu for GLU weights (row blocks of the packed
+ * order). w_out holds ifx_fp8_skinny_tiled_bytes(N, K) bytes; scales and bias
+ * are unchanged. No counterpart in the reference (a layout of this build).
+ */
+size_t ifx_fp8_skinny_tiled_bytes(int64_t N, int64_t K);
+int ifx_fp8_pack_skinny(const void* w, int64_t ldw, int64_t N, int64_t K, void* w_out, void* stream);
 
 /*
  * Repack a gate|up weight (rows [0,F) gate, [F,2F) up; e4m3 [2F,K] + f32 scale

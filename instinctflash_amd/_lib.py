@@ -40,6 +40,7 @@ EPI_OUT_F32 = 64
 EPI_RES_F32 = 128
 EPI_SCALAR_SA = 256
 EPI_SCALAR_SW = 512
+EPI_W_TILED = 1024
 RNQ_WRITE_RES = 1
 RNQ_LAYERNORM = 2
 SCALE_ROW = 0
@@ -63,6 +64,8 @@ SIGNATURES = {
     "ifx_dequant_rows": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P]),
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
+    "ifx_fp8_skinny_tiled_bytes": (_SZ, [_I64, _I64]),
+    "ifx_fp8_pack_skinny": (_INT, [_P, _I64, _I64, _I64, _P, _P]),
     "ifx_residual_norm_quant": (_INT, [_P, _INT, _I64, _P, _INT, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _INT,
                                        ctypes.c_float, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _P]),
     "ifx_quant_linear": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64, _I64,

@@ -902,7 +902,10 @@ __device__ __forceinline__ v4f load_agent4(const float* p) {
   return v;
 }
 
-template <int MB, int NBW, int WAVES>
+// TILED: w is in the layout of ifx_fp8_pack_skinny (2 KB tile per 16-row block
+// and 128-byte K step, zero-padded in K), so each weight load instruction of a
+// wave reads 1 KB of contiguous memory.
+template <int MB, int NBW, int WAVES, bool TILED>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
                                                           const uint8_t* __restrict__ W, int64_t ldw,
                                                           int64_t K, Epi e, SkSplit sp) {
@@ -976,11 +979,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
       const bool hi = s < s_end && k0 + 16 < K;
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
-        const uint8_t* p = wrow[b] + s * kBK;
 #ifdef IFX_DBG_SK_NO_W
         wf[u][b] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
 #else
-        wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
+        if constexpr (TILED) {
+          const bool in = s < s_end;
+          const uint8_t* p = W + ((grp * NBW + b) * ksteps + s) * 2048 + lane * 16;
+          wf[u][b] = cat8(in ? ld16_nt(p) : v4i{0, 0, 0, 0}, in ? ld16_nt(p + 1024) : v4i{0, 0, 0, 0});
+        } else {
+          const uint8_t* p = wrow[b] + s * kBK;
+          wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
+        }
 #endif
       }
 #pragma unroll
@@ -1138,8 +1147,11 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
 template <int MB, int NBW, int WAVES>
 void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
                      const Epi& e, const SkSplit& sp, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES>), dim3(static_cast<unsigned>(p.groups * p.ksplit)),
-                     dim3(WAVES * 64), 0, st, a, lda, w, ldw, K, e, sp);
+  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit)), block(WAVES * 64);
+  if (e.flags & IFX_EPI_W_TILED)
+    hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, true>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
+  else
+    hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, false>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
 }
 
 template <int MB, int NBW>
@@ -1181,6 +1193,24 @@ int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint
 }
 
 constexpr int64_t kSkinnyMaxM = 64;
+
+// One thread per 16-byte chunk of the tiled layout: chunk c = ((b * ks + s) *
+// 2 + half) * 64 + l holds row 16b + l%16, K bytes s*128 + 32*(l/16) + 16*half
+// + 0..15 (zero past K).
+__global__ __launch_bounds__(256) void pack_skinny_kernel(const uint8_t* __restrict__ w, int64_t ldw, int64_t K,
+                                                          int64_t ks, int64_t chunks, uint8_t* __restrict__ out) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int l = static_cast<int>(c & 63);
+  const int half = static_cast<int>((c >> 6) & 1);
+  const int64_t bs = c >> 7;  // b * ks + s
+  const int64_t b = bs / ks, st = bs - b * ks;
+  const int64_t row = b * 16 + (l & 15);
+  const int64_t k = st * kBK + 32 * (l >> 4) + 16 * half;
+  v4i v{0, 0, 0, 0};
+  if (k < K) v = *reinterpret_cast<const v4i*>(w + row * ldw + k);
+  *reinterpret_cast<v4i*>(out + c * 16) = v;
+}
 
 // Large-M configurations:
 //  * wide:   256 x 256 tiles, 8 waves, 128-byte K stages, 2-deep ring
@@ -1232,15 +1262,17 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
                  const void* gate, int epilogue, const void* out, int64_t ldo, int64_t M, int64_t N, int64_t K) {
   constexpr int kKnown = IFX_EPI_BIAS | IFX_EPI_GELU_TANH | IFX_EPI_GEGLU | IFX_EPI_SWIGLU |
                          IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32 |
-                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW;
+                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW | IFX_EPI_W_TILED;
   if (epilogue & ~kKnown) return IFX_ERR_INVALID;
   const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
+  const bool tiled = (epilogue & IFX_EPI_W_TILED) != 0;
+  if (tiled && M > kSkinnyMaxM) return IFX_ERR_UNSUPPORTED;  // the tile layout serves M <= 64
   if ((epilogue & IFX_EPI_GEGLU) && (epilogue & IFX_EPI_SWIGLU)) return IFX_ERR_INVALID;
   if (glu && (epilogue & IFX_EPI_GELU_TANH)) return IFX_ERR_INVALID;
   if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0) return IFX_ERR_INVALID;
   if (glu && N % 32 != 0) return IFX_ERR_INVALID;
   const int64_t n_out = glu ? N / 2 : N;
-  if (ldw < K || ldo < n_out) return IFX_ERR_INVALID;
+  if ((!tiled && ldw < K) || ldo < n_out) return IFX_ERR_INVALID;
   if (M == 0) return IFX_OK;
   if (!w || !out) return IFX_ERR_INVALID;
   if ((epilogue & IFX_EPI_BIAS) && !bias) return IFX_ERR_INVALID;
@@ -1248,7 +1280,7 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
   if (epilogue & IFX_EPI_RESIDUAL) {
     if (!residual || ldr < n_out || ldr % 8 != 0 || !aligned16(residual)) return IFX_ERR_INVALID;
   }
-  if (!aligned16(w) || !aligned16(out) || ldw % 16 != 0 || ldo % 8 != 0) return IFX_ERR_ALIGN;
+  if (!aligned16(w) || !aligned16(out) || (!tiled && ldw % 16 != 0) || ldo % 8 != 0) return IFX_ERR_ALIGN;
   if ((sw && !(epilogue & IFX_EPI_SCALAR_SW) && !aligned16(sw)) || (bias && !aligned16(bias)) ||
       (gate && (reinterpret_cast<uintptr_t>(gate) & 7u)))
     return IFX_ERR_ALIGN;
@@ -1305,6 +1337,24 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
+}
+
+size_t ifx_fp8_skinny_tiled_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0) return 0;
+  return static_cast<size_t>(N / 16) * ((K + kBK - 1) / kBK) * 2048;
+}
+
+int ifx_fp8_pack_skinny(const void* w, int64_t ldw, int64_t N, int64_t K, void* w_out, void* stream) {
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0 || ldw < K) return IFX_ERR_INVALID;
+  if (!w || !w_out) return IFX_ERR_INVALID;
+  if (!aligned16(w) || !aligned16(w_out) || ldw % 16 != 0) return IFX_ERR_ALIGN;
+  const int64_t ks = (K + kBK - 1) / kBK;
+  const int64_t chunks = (N / 16) * ks * 128;
+  if ((chunks + 255) / 256 > 0x7FFFFFFFLL) return IFX_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(pack_skinny_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w), ldw, K, ks, chunks,
+                     static_cast<uint8_t*>(w_out));
+  return launch_status();
 }
 
 size_t ifx_quant_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode) {

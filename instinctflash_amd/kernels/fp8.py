@@ -4,8 +4,8 @@ with fused epilogue, on gfx950 HIP kernels.
 Public names mirror the reference module instinctflash/kernels/fp8.py
 (``E4M3``, ``FP8_MAX``, ``Fp8Weight``, ``quantize_weight``, ``gemm``) so an
 engine that imports them runs unchanged; ``quant_rows``, ``linear``,
-``pack_glu``, ``quantize_tensor`` and ``quant_linear`` are the fused entry points of
-this build.
+``pack_glu``, ``pack_skinny``, ``quantize_tensor`` and ``quant_linear`` are the fused
+entry points of this build.
 
 Every call validates its tensors on the host and raises ``ValueError`` before
 anything is launched; kernels run on the current HIP stream and never allocate
@@ -33,16 +33,20 @@ class Fp8Weight:
     ``w`` [N, K] E4M3, K contiguous; ``scale`` [N] FP32 per-output-channel
     dequantization scale; ``bias`` [N] FP32 or None. ``glu`` marks a gate|up
     weight already repacked by :func:`pack_glu` (rows interleaved in blocks of 16).
+    ``tiled`` marks a weight repacked by :func:`pack_skinny` for M <= 64 calls:
+    ``w`` then holds 2 KB fragment tiles and ``nk`` the logical (N, K).
     """
 
     w: torch.Tensor
     scale: torch.Tensor
     bias: torch.Tensor | None = None
     glu: bool = False
+    tiled: bool = False
+    nk: tuple | None = None
 
     @property
     def shape(self):
-        return tuple(self.w.shape)
+        return tuple(self.nk) if self.tiled else tuple(self.w.shape)
 
 
 # ---------------------------------------------------------------------------
@@ -185,7 +189,17 @@ def pack_tensor(x: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
 def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales):
     """Validates the weight, output and epilogue operands of a projection of M
     rows; returns (flags, N, ldw, sw, bias, ldr, ldo)."""
-    N, Kw, ldw = _rows("w.w", w.w, E4M3, device)
+    if w.tiled:
+        N, Kw = w.nk
+        _on_device("w.w", w.w, device)
+        if w.w.dtype != E4M3 or not w.w.is_contiguous() or w.w.numel() != _lib.load().ifx_fp8_skinny_tiled_bytes(N, Kw):
+            raise ValueError("w.w is not a pack_skinny tile array for the recorded (N, K)")
+        if M > 64:
+            raise ValueError("a pack_skinny weight serves M <= 64 only")
+        ldw = 0
+        flags |= _lib.EPI_W_TILED
+    else:
+        N, Kw, ldw = _rows("w.w", w.w, E4M3, device)
     if Kw != K:
         raise ValueError(f"the activations have K={K} but the weight has K={Kw}")
     glu = bool(flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU))
@@ -233,7 +247,7 @@ def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales
         for name, t in (("w.w", w.w), ("out", out)):
             if t.data_ptr() % 16:
                 raise ValueError(f"{name} must be 16-byte aligned")
-        if ldw % 16 or ldo % 8 or (residual is not None and (ldr % 8 or residual.data_ptr() % 16)):
+        if (not w.tiled and ldw % 16) or ldo % 8 or (residual is not None and (ldr % 8 or residual.data_ptr() % 16)):
             raise ValueError("row strides must be multiples of 16 bytes (w) and 8 elements (out, residual)")
     return flags, N, ldw, sw, bias, ldr, ldo
 
@@ -289,7 +303,7 @@ def linear(a: torch.Tensor, a_scale: torch.Tensor, w: Fp8Weight, out: torch.Tens
         raise ValueError(f"unknown activation {act!r}; expected one of {sorted(k for k in ACTIVATIONS if k)}")
     flags = ACTIVATIONS[act]
     if out is None:
-        n_out = w.w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.w.shape[0]
+        n_out = w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.shape[0]
         out = torch.empty((a.shape[0], n_out), dtype=out_dtype, device=a.device)
     return _linear(a, a_scale, w, out, flags, residual=residual, gate=gate)
 
@@ -310,7 +324,7 @@ def quant_linear(x: torch.Tensor, w: Fp8Weight, out: torch.Tensor | None = None,
     M, K, ldx = _rows("x", x, torch.bfloat16)
     flags = ACTIVATIONS[act]
     if out is None:
-        n_out = w.w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.w.shape[0]
+        n_out = w.shape[0] // 2 if flags & (_lib.EPI_GEGLU | _lib.EPI_SWIGLU) else w.shape[0]
         out = torch.empty((M, n_out), dtype=out_dtype, device=x.device)
     flags, N, ldw, sw, bias, ldr, ldo = _epilogue(M, K, x.device, w, out, flags, residual, gate, True)
     mode = _lib.SCALE_TENSOR if per_tensor else _lib.SCALE_ROW
@@ -338,6 +352,8 @@ def pack_glu(w: Fp8Weight) -> Fp8Weight:
     of the fused GLU epilogue. Output width of the projection is F."""
     if w.glu:
         return w
+    if w.tiled:
+        raise ValueError("pack_glu must come before pack_skinny")
     N, K, ldw = _rows("w.w", w.w, E4M3)
     if N % 32 or ldw != K:
         raise ValueError("pack_glu needs a contiguous [2F, K] weight with F % 16 == 0")
@@ -350,3 +366,22 @@ def pack_glu(w: Fp8Weight) -> Fp8Weight:
     _lib.check(_lib.load().ifx_fp8_pack_glu(_ptr(w.w), _ptr(w.scale), _ptr(w.bias), N // 2, K, _ptr(wo),
                                             _ptr(so), _ptr(bo), _stream(w.w.device)), "ifx_fp8_pack_glu")
     return Fp8Weight(wo, so, bo, glu=True)
+
+
+def pack_skinny(w: Fp8Weight) -> Fp8Weight:
+    """Repack a weight for M <= 64 projections (decode / action-head shapes): each
+    16-row block and 128-byte K step becomes one contiguous 2 KB tile in the order
+    the matrix-core fragments are loaded, so every load instruction of the skinny
+    GEMM reads 1 KB of contiguous memory. Scales, bias and the GLU flag carry
+    over; apply after :func:`pack_glu`. Such a weight is rejected for M > 64."""
+    if w.tiled:
+        return w
+    N, K, ldw = _rows("w.w", w.w, E4M3)
+    if N % 16 or K % 16:
+        raise ValueError("pack_skinny needs N % 16 == 0 and K % 16 == 0")
+    if w.w.data_ptr() % 16 or ldw % 16:
+        raise ValueError("w.w must be 16-byte aligned with a 16-byte multiple row stride")
+    lib = _lib.load()
+    out = torch.empty(lib.ifx_fp8_skinny_tiled_bytes(N, K), dtype=E4M3, device=w.w.device)
+    _lib.check(lib.ifx_fp8_pack_skinny(_ptr(w.w), ldw, N, K, _ptr(out), _stream(w.w.device)), "ifx_fp8_pack_skinny")
+    return Fp8Weight(out, w.scale, w.bias, glu=w.glu, tiled=True, nk=(N, K))

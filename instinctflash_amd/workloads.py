@@ -124,6 +124,12 @@ def _weights(g, N, K, dev, bias=False, glu=False):
     return F.pack_glu(fw) if glu else fw
 
 
+def _copies(fw, n):
+    """fw and n-1 clones: identical numerics, distinct HBM lines."""
+    return [fw] + [F.Fp8Weight(fw.w.clone(), fw.scale.clone(), None if fw.bias is None else fw.bias.clone(),
+                               glu=fw.glu, tiled=fw.tiled, nk=fw.nk) for _ in range(n - 1)]
+
+
 def _pool_size(bytes_per_set: int) -> int:
     return max(1, -(-(INFINITY_CACHE_BYTES + (32 << 20)) // bytes_per_set))
 
@@ -148,9 +154,9 @@ class C1(Workload):
         g = _gen(seed)
         x = _act(g, M, K, outlier_frac=0.01)
         self.pool = pool or _pool_size(N * K)
-        ws = [_weights(g, N, K, dev, bias=True)]
-        # Rotated copies of the same quantized weight: identical numerics, distinct HBM lines.
-        ws += [F.Fp8Weight(ws[0].w.clone(), ws[0].scale.clone(), ws[0].bias.clone()) for _ in range(self.pool - 1)]
+        # M <= 64 weights are packed once into the skinny tile layout; rotated
+        # copies give identical numerics on distinct HBM lines.
+        ws = _copies(F.pack_skinny(_weights(g, N, K, dev, bias=True)), self.pool)
         b = _Buffers(dev)
         self.tensors = dict(x=x.to(torch.bfloat16).to(dev), w=ws, qa=b.q(M, K),
                             out=torch.empty((M, N), dtype=torch.bfloat16, device=dev))
@@ -182,8 +188,8 @@ class C2(Workload):
         w2 = _weights(g, D, FF, dev)
         res = torch.randn((M, D), generator=g).to(torch.bfloat16)
         self.pool = pool or _pool_size(2 * FF * D)
-        w1s = [w1] + [F.Fp8Weight(w1.w.clone(), w1.scale.clone()) for _ in range(self.pool - 1)]
-        w2s = [w2] + [F.Fp8Weight(w2.w.clone(), w2.scale.clone()) for _ in range(self.pool - 1)]
+        w1s = _copies(F.pack_skinny(w1), self.pool)
+        w2s = _copies(F.pack_skinny(w2), self.pool)
         b = _Buffers(dev)
         self.tensors = dict(xs=[x.to(torch.bfloat16).to(dev) for x in xs], w1=w1s, w2=w2s, res=res.to(dev),
                             q1=b.q(M, D), q2=b.q(M, FF), h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),

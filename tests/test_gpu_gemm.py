@@ -314,3 +314,61 @@ def test_skinny_split_k(gpu, oracle_mod, M, N, K, act):
     r = res.to(gpu).clone()
     F.linear(qa, sa, w, out=r, act=act, residual=r)
     assert torch.equal(r.view(torch.int16), o16.view(torch.int16))
+
+
+def _tile_layout_np(w, K):
+    """Numpy restatement of the pack_skinny layout (ifx_fp8.h): tile (b, s) holds, for
+    lane l, row 16b + l%16 K bytes [128s + 32(l/16), +16) at 16l and the next 16 at 1024+16l."""
+    N = w.shape[0]
+    ks = -(-K // 128)
+    wp = np.zeros((N, ks * 128), np.uint8)
+    wp[:, :K] = w[:, :K]
+    out = np.zeros((N // 16, ks, 2, 64, 16), np.uint8)
+    for l in range(64):
+        rows = np.arange(N // 16) * 16 + (l % 16)
+        for half in range(2):
+            for s in range(ks):
+                k0 = 128 * s + 32 * (l // 16) + 16 * half
+                out[:, s, half, l] = wp[rows, k0:k0 + 16]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("M,N,K,act", [(16, 6144, 1536, "gelu_tanh"), (16, 1536, 6144, None), (50, 4096, 1024, None),
+                                       (1, 16, 128, None), (33, 48, 176, None), (16, 2048, 1536, "geglu"),
+                                       (13, 4096, 16384, "swiglu"), (64, 256, 2064, "gelu_tanh")])
+def test_skinny_tiled_weights(gpu, M, N, K, act):
+    # pack_skinny: the tile bytes follow the documented layout, and the projection is
+    # bit-identical to the row-major weight's (same bytes in the same fragment slots)
+    from instinctflash_amd.kernels import fp8 as F, pack_glu, pack_skinny
+    glu = act in ("geglu", "swiglu")
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=N + K, bias=True)
+    w = pack_glu(fw) if glu else fw
+    wt = pack_skinny(w)
+    assert wt.tiled and wt.shape == (N, K) and wt.glu == glu
+    assert np.array_equal(_q(wt.w), _tile_layout_np(_q(w.w), K))
+    n_out = N // 2 if glu else N
+    res = torch.randn((M, n_out), generator=g).to(torch.bfloat16).to(gpu)
+    gate = torch.rand(n_out, generator=g).to(torch.bfloat16).to(gpu)
+    for dt in (torch.bfloat16, torch.float32):
+        ref = F.linear(qa, sa, w, act=act, residual=res, gate=gate, out_dtype=dt)
+        got = F.linear(qa, sa, wt, act=act, residual=res, gate=gate, out_dtype=dt)
+        iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+        assert torch.equal(got.view(iv), ref.view(iv)), f"tiled {M}x{N}x{K} {act} {dt}"
+    if not glu:
+        raw_ref = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+        raw = torch.empty_like(raw_ref)
+        F.gemm(qa, fw, raw_ref)
+        F.gemm(qa, wt, raw)
+        assert torch.equal(raw.view(torch.int16), raw_ref.view(torch.int16))
+
+
+def test_skinny_tiled_contract(gpu):
+    from instinctflash_amd.kernels import fp8 as F, pack_glu, pack_skinny
+    qa, sa, fw, g = _make(gpu, 16, 256, 512, seed=1)
+    wt = pack_skinny(fw)
+    big = torch.zeros((65, 512), dtype=torch.float8_e4m3fn, device=gpu)
+    with pytest.raises(ValueError, match="M <= 64"):
+        F.linear(big, torch.ones(65, device=gpu), wt)
+    with pytest.raises(ValueError, match="before pack_skinny"):
+        pack_glu(wt)
+    assert pack_skinny(wt) is wt
