@@ -79,6 +79,9 @@ extern "C" {
 /* w is in the skinny tile layout written by ifx_fp8_pack_skinny (M <= 64 only;
  * ldw is ignored). Not an epilogue option, but carried in the same flags. */
 #define IFX_EPI_W_TILED 1024
+/* a is in the skinny tile layout written by ifx_quant_rows_tiled (M <= 64 only;
+ * lda is ignored). */
+#define IFX_EPI_A_TILED 2048
 
 int ifx_abi_version(void);
 /* Host pointer to a static string describing a status code. */
@@ -229,6 +232,19 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
                      const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
                      void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
                      size_t ws_bytes, void* stream);
+
+/*
+ * ifx_quant_rows for M <= 64 rows (K % 16 == 0, K <= 16384) writing q in the
+ * skinny tile layout of ifx_fp8_pack_skinny (tokens in place of weight rows:
+ * block j = rows 16j..16j+15), zero-filled past M and K, so a following
+ * ifx_fp8_linear with IFX_EPI_A_TILED reads 1 KB contiguous per load
+ * instruction. Same bytes and scales as ifx_quant_rows, only placed
+ * differently. q holds ifx_quant_rows_tiled_bytes(M, K) bytes, 16-byte aligned.
+ * No counterpart in the reference (a layout of this build).
+ */
+size_t ifx_quant_rows_tiled_bytes(int64_t M, int64_t K);
+int ifx_quant_rows_tiled(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, void* q, float* scale,
+                         void* stream);
 
 /*
  * Repack an e4m3 weight [N, K] (row stride ldw; N % 16 == 0, K % 16 == 0) into

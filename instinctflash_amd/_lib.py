@@ -41,6 +41,7 @@ EPI_RES_F32 = 128
 EPI_SCALAR_SA = 256
 EPI_SCALAR_SW = 512
 EPI_W_TILED = 1024
+EPI_A_TILED = 2048
 RNQ_WRITE_RES = 1
 RNQ_LAYERNORM = 2
 SCALE_ROW = 0
@@ -65,6 +66,8 @@ SIGNATURES = {
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
     "ifx_fp8_skinny_tiled_bytes": (_SZ, [_I64, _I64]),
+    "ifx_quant_rows_tiled_bytes": (_SZ, [_I64, _I64]),
+    "ifx_quant_rows_tiled": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P]),
     "ifx_fp8_pack_skinny": (_INT, [_P, _I64, _I64, _I64, _P, _P]),
     "ifx_residual_norm_quant": (_INT, [_P, _INT, _I64, _P, _INT, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _INT,
                                        ctypes.c_float, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _P]),

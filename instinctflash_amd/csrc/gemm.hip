@@ -923,6 +923,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const int64_t ksteps = (K + kBK - 1) / kBK;
   const int64_t s_begin = slice * sp.kss;
   const int64_t s_end = min(s_begin + sp.kss, ksteps);
+  const bool a_tiled = (e.flags & IFX_EPI_A_TILED) != 0;  // A in the skinny tile layout (lda unused)
 
   const uint8_t* wrow[NBW];
 #pragma unroll
@@ -998,7 +999,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #ifdef IFX_DBG_SK_NO_A
         af[u][j] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
 #else
-        af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
+        if (a_tiled) {  // workgroup-uniform
+          const bool in = s < s_end;
+          const uint8_t* t = A + (j * ksteps + s) * 2048 + lane * 16;
+          af[u][j] = cat8(in ? ld16(t) : v4i{0, 0, 0, 0}, in ? ld16(t + 1024) : v4i{0, 0, 0, 0});
+        } else {
+          af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
+        }
 #endif
       }
     }
@@ -1262,11 +1269,12 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
                  const void* gate, int epilogue, const void* out, int64_t ldo, int64_t M, int64_t N, int64_t K) {
   constexpr int kKnown = IFX_EPI_BIAS | IFX_EPI_GELU_TANH | IFX_EPI_GEGLU | IFX_EPI_SWIGLU |
                          IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32 |
-                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW | IFX_EPI_W_TILED;
+                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW | IFX_EPI_W_TILED | IFX_EPI_A_TILED;
   if (epilogue & ~kKnown) return IFX_ERR_INVALID;
   const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
   const bool tiled = (epilogue & IFX_EPI_W_TILED) != 0;
-  if (tiled && M > kSkinnyMaxM) return IFX_ERR_UNSUPPORTED;  // the tile layout serves M <= 64
+  // the tile layouts serve M <= 64
+  if ((tiled || (epilogue & IFX_EPI_A_TILED)) && M > kSkinnyMaxM) return IFX_ERR_UNSUPPORTED;
   if ((epilogue & IFX_EPI_GEGLU) && (epilogue & IFX_EPI_SWIGLU)) return IFX_ERR_INVALID;
   if (glu && (epilogue & IFX_EPI_GELU_TANH)) return IFX_ERR_INVALID;
   if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0) return IFX_ERR_INVALID;
@@ -1316,10 +1324,11 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                    int64_t K, void* workspace, size_t ws_bytes, void* stream) {
   const int rc = check_linear(w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (lda < K) return IFX_ERR_INVALID;
+  const bool a_tiled = (epilogue & IFX_EPI_A_TILED) != 0;
+  if (!a_tiled && lda < K) return IFX_ERR_INVALID;
   if (M == 0) return IFX_OK;
   if (!a) return IFX_ERR_INVALID;
-  if (!aligned16(a) || lda % 16 != 0) return IFX_ERR_ALIGN;
+  if (!aligned16(a) || (!a_tiled && lda % 16 != 0)) return IFX_ERR_ALIGN;
   const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
 
   Epi e{sa, sw, bias, residual, ldr, static_cast<const uint16_t*>(gate), out, ldo, epilogue, M, N};

@@ -18,6 +18,8 @@
 //    propagates NaN exactly as torch's amax does.
 //  * 128-bit loads, 64-bit stores of 8 packed E4M3 codes, scale written once.
 
+#include <type_traits>
+
 #include "ifx_abi.h"
 #include "ifx_device.h"
 #include "ifx_quant.h"
@@ -135,9 +137,20 @@ __device__ __forceinline__ uint32_t team_max(uint32_t v, uint32_t* red) {
 
 // Register-resident row quantizer: K % 8 == 0, 16-byte aligned rows,
 // ceil(K/8) <= T*VPT.
+// Byte offset of element (m, k) (k % 8 == 0) in the skinny tile layout with ks
+// K steps per 16-row block: tile (m/16, k/128) of 2 KB, lane l = 16*((k%128)/32)
+// + m%16 holds K bytes [32*(l/16), +16) at 16l and the next 16 at 1024 + 16l.
+__device__ __forceinline__ int64_t tile_offset(int64_t m, int64_t k, int64_t ks) {
+  return ((m >> 4) * ks + (k >> 7)) * 2048 + ((k >> 4) & 1) * 1024 + ((((k >> 5) & 3) << 4) + (m & 15)) * 16 +
+         (k & 15);
+}
+
+// ks == 0: q is row-major with stride ldq. ks > 0: q is the skinny tile layout
+// (rows M..16*ceil(M/16)-1 and K bytes K..128*ks-1 are written as zeros, by the
+// launch covering m_rows = 16*ceil(M/16) rows).
 template <int T, int VPT, class Src>
 __global__ __launch_bounds__(kBlock) void quant_rows_vec(Src src, int64_t M, int64_t K, uint8_t* q,
-                                                        int64_t ldq, float* scale) {
+                                                        int64_t ldq, float* scale, int64_t ks, int64_t m_rows) {
   __shared__ uint32_t red[kBlock / 64];
   constexpr int R = kBlock / T;
   const int lt = threadIdx.x % T;
@@ -159,21 +172,28 @@ __global__ __launch_bounds__(kBlock) void quant_rows_vec(Src src, int64_t M, int
     }
   }
   amax = team_max<T>(amax, red);
+  if (ks > 0 && m < m_rows) {  // zero padding of the tile layout
+    for (int64_t idx = row_ok ? nvec + lt : lt; idx < ks * 16; idx += T)
+      *reinterpret_cast<uint2*>(q + tile_offset(m, idx * 8, ks)) = make_uint2(0u, 0u);
+  }
   if (!row_ok) return;
   const float s = scale_from_amax_bits(amax);
   if (lt == 0) scale[m] = s;
+  auto dst = [&](int64_t idx) -> uint2* {
+    return reinterpret_cast<uint2*>(q + (ks > 0 ? tile_offset(m, idx * 8, ks) : m * ldq + idx * 8));
+  };
   if (finite_scale(s)) {  // row-uniform branch
     const float r = 1.0f / s;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t idx = lt + static_cast<int64_t>(j) * T;
-      if (idx < nvec) *reinterpret_cast<uint2*>(q + m * ldq + idx * 8) = pack8_fast(v[j], s, r);
+      if (idx < nvec) *dst(idx) = pack8_fast(v[j], s, r);
     }
   } else {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int64_t idx = lt + static_cast<int64_t>(j) * T;
-      if (idx < nvec) *reinterpret_cast<uint2*>(q + m * ldq + idx * 8) = pack8_exact(v[j], s);
+      if (idx < nvec) *dst(idx) = pack8_exact(v[j], s);
     }
   }
 }
@@ -198,11 +218,12 @@ __global__ __launch_bounds__(kBlock) void quant_rows_generic(Src src, int64_t M,
 
 template <int T, int VPT, class Src>
 void launch_vec(const Src& src, int64_t M, int64_t K, uint8_t* q, int64_t ldq, float* scale,
-                hipStream_t st) {
+                hipStream_t st, int64_t ks = 0) {
   constexpr int R = kBlock / T;
-  const int64_t grid = (M + R - 1) / R;
+  const int64_t m_rows = ks > 0 ? (M + 15) / 16 * 16 : M;
+  const int64_t grid = (m_rows + R - 1) / R;
   hipLaunchKernelGGL((quant_rows_vec<T, VPT, Src>), dim3(static_cast<unsigned>(grid)), dim3(kBlock),
-                     0, st, src, M, K, q, ldq, scale);
+                     0, st, src, M, K, q, ldq, scale, ks, m_rows);
 }
 
 // Picks the register-resident variant (team size, vectors per lane) or falls
@@ -383,6 +404,35 @@ const char* ifx_status_string(int status) {
     case IFX_ERR_UNSUPPORTED: return "shape not supported by any kernel variant";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
   }
+}
+
+size_t ifx_quant_rows_tiled_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || M > 64 || K % 16 != 0) return 0;
+  return static_cast<size_t>((M + 15) / 16) * ((K + 127) / 128) * 2048;
+}
+
+int ifx_quant_rows_tiled(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, void* q, float* scale,
+                         void* stream) {
+  if (x_dtype != IFX_DTYPE_BF16 && x_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
+  if (M < 0 || M > 64 || K <= 0 || K % 16 != 0 || ldx < K) return IFX_ERR_INVALID;
+  if (M == 0) return IFX_OK;
+  if (!x || !q || !scale) return IFX_ERR_INVALID;
+  const bool f32 = x_dtype == IFX_DTYPE_F32;
+  if (!aligned16(x) || !aligned16(q) || ldx % (f32 ? 4 : 8) != 0) return IFX_ERR_ALIGN;
+  const int64_t nvec = K / 8, ks = (K + 127) / 128;
+  if (nvec > 2048) return IFX_ERR_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* qb = static_cast<uint8_t*>(q);
+  auto go = [&](const auto& src) {
+    using S = std::decay_t<decltype(src)>;
+    if (nvec <= 256) launch_vec<256, 1, S>(src, M, K, qb, 0, scale, st, ks);
+    else if (nvec <= 512) launch_vec<256, 2, S>(src, M, K, qb, 0, scale, st, ks);
+    else if (nvec <= 1024) launch_vec<256, 4, S>(src, M, K, qb, 0, scale, st, ks);
+    else launch_vec<256, 8, S>(src, M, K, qb, 0, scale, st, ks);
+  };
+  if (f32) go(SrcF32{static_cast<const float*>(x), ldx});
+  else go(SrcBf16{static_cast<const uint16_t*>(x), ldx});
+  return launch_status();
 }
 
 int ifx_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, void* q,

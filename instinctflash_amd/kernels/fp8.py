@@ -49,6 +49,26 @@ class Fp8Weight:
         return tuple(self.nk) if self.tiled else tuple(self.w.shape)
 
 
+@dataclass
+class TiledRows:
+    """E4M3 activations [M, K] (M <= 64) in the skinny tile layout written by
+    :func:`quant_rows_tiled`: ``q`` holds the tiles, ``M`` / ``K`` the logical
+    shape. Accepted by :func:`linear` and :func:`gemm` wherever an [M, K] e4m3
+    tensor is."""
+
+    q: torch.Tensor
+    M: int
+    K: int
+
+    @property
+    def shape(self):
+        return (self.M, self.K)
+
+    @property
+    def device(self):
+        return self.q.device
+
+
 # ---------------------------------------------------------------------------
 # helpers
 # ---------------------------------------------------------------------------
@@ -136,6 +156,30 @@ def quant_rows(x: torch.Tensor, q: torch.Tensor | None = None, scale: torch.Tens
     dt = _lib.DTYPE_BF16 if x.dtype == torch.bfloat16 else _lib.DTYPE_F32
     _lib.check(_lib.load().ifx_quant_rows(_ptr(x), dt, ldx, M, K, _ptr(q), ldq, _ptr(scale),
                                           _stream(x.device)), "ifx_quant_rows")
+    return q, scale
+
+
+def quant_rows_tiled(x: torch.Tensor, q: TiledRows | None = None, scale: torch.Tensor | None = None):
+    """``quant_rows`` for M <= 64 rows, writing the skinny tile layout that the
+    M <= 64 GEMM reads with 1 KB contiguous loads: same bytes and scales, only
+    placed differently. Returns (TiledRows, scale)."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"quant_rows_tiled expects bf16 or fp32 input, got {x.dtype}")
+    M, K, ldx = _rows("x", x, x.dtype)
+    if not 0 < M <= 64 or K % 16:
+        raise ValueError("quant_rows_tiled needs 1 <= M <= 64 and K % 16 == 0")
+    lib = _lib.load()
+    nbytes = lib.ifx_quant_rows_tiled_bytes(M, K)
+    if q is None:
+        q = TiledRows(torch.empty(nbytes, dtype=E4M3, device=x.device), M, K)
+    if (q.M, q.K) != (M, K) or q.q.numel() != nbytes or q.q.dtype != E4M3 or q.device != x.device:
+        raise ValueError("q does not hold the tile layout of x's shape")
+    if scale is None:
+        scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _vec("scale", scale, M, device=x.device)
+    dt = _lib.DTYPE_BF16 if x.dtype == torch.bfloat16 else _lib.DTYPE_F32
+    _lib.check(lib.ifx_quant_rows_tiled(_ptr(x), dt, ldx, M, K, _ptr(q.q), _ptr(scale), _stream(x.device)),
+               "ifx_quant_rows_tiled")
     return q, scale
 
 
@@ -253,7 +297,14 @@ def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales
 
 
 def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scales=True):
-    M, K, lda = _rows("a", a, E4M3)
+    if isinstance(a, TiledRows):
+        M, K, lda = a.M, a.K, 0
+        _on_device("a", a.q)
+        flags |= _lib.EPI_A_TILED
+        a_t = a.q
+    else:
+        M, K, lda = _rows("a", a, E4M3)
+        a_t = a
     flags, N, ldw, sw, bias, ldr, ldo = _epilogue(M, K, a.device, w, out, flags, residual, gate, use_scales)
     if use_scales:
         # per-token [M] scales or one shared value
@@ -264,13 +315,13 @@ def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scale
             _vec("a_scale", sa, M, device=a.device)
     if M == 0:
         return out
-    if a.data_ptr() % 16 or lda % 16:
+    if a_t.data_ptr() % 16 or lda % 16:
         raise ValueError("a must be 16-byte aligned with a row stride that is a multiple of 16 bytes")
     lib = _lib.load()
     stream = _stream(a.device)
     nbytes = lib.ifx_fp8_linear_workspace_size(M, N, K, flags)
     ws = _workspace(nbytes, a.device, stream)
-    _lib.check(lib.ifx_fp8_linear(_ptr(a), lda, _ptr(sa) if use_scales else None, _ptr(w.w), ldw,
+    _lib.check(lib.ifx_fp8_linear(_ptr(a_t), lda, _ptr(sa) if use_scales else None, _ptr(w.w), ldw,
                                   _ptr(sw), _ptr(bias), _ptr(residual), ldr, _ptr(gate), flags,
                                   _ptr(out), ldo, M, N, K, _ptr(ws), nbytes, stream), "ifx_fp8_linear")
     return out

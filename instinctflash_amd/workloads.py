@@ -157,14 +157,14 @@ class C1(Workload):
         # M <= 64 weights are packed once into the skinny tile layout; rotated
         # copies give identical numerics on distinct HBM lines.
         ws = _copies(F.pack_skinny(_weights(g, N, K, dev, bias=True)), self.pool)
-        b = _Buffers(dev)
-        self.tensors = dict(x=x.to(torch.bfloat16).to(dev), w=ws, qa=b.q(M, K),
+        xb = x.to(torch.bfloat16).to(dev)
+        self.tensors = dict(x=xb, w=ws, qa=F.quant_rows_tiled(xb),
                             out=torch.empty((M, N), dtype=torch.bfloat16, device=dev))
 
     def _run(self, p):
         t = self.tensors
         qa, sa = t["qa"]
-        F.quant_rows(t["x"], qa, sa)
+        F.quant_rows_tiled(t["x"], qa, sa)  # M <= 64: activations in the skinny tile layout
         F.linear(qa, sa, t["w"][p], out=t["out"])
 
     def dominant_call(self, p):
@@ -190,9 +190,10 @@ class C2(Workload):
         self.pool = pool or _pool_size(2 * FF * D)
         w1s = _copies(F.pack_skinny(w1), self.pool)
         w2s = _copies(F.pack_skinny(w2), self.pool)
-        b = _Buffers(dev)
-        self.tensors = dict(xs=[x.to(torch.bfloat16).to(dev) for x in xs], w1=w1s, w2=w2s, res=res.to(dev),
-                            q1=b.q(M, D), q2=b.q(M, FF), h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
+        xsd = [x.to(torch.bfloat16).to(dev) for x in xs]
+        h = torch.empty((M, FF), dtype=torch.bfloat16, device=dev)
+        self.tensors = dict(xs=xsd, w1=w1s, w2=w2s, res=res.to(dev), q1=F.quant_rows_tiled(xsd[0]),
+                            q2=F.quant_rows_tiled(h.zero_()), h=h,
                             out=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
 
     def _run(self, p):
@@ -200,11 +201,12 @@ class C2(Workload):
         q1, s1 = t["q1"]
         q2, s2 = t["q2"]
         for s in range(4):
-            # one weight set per (step, flow step): a deep DiT streams each layer's weights
+            # one weight set per (step, flow step): a deep DiT streams each layer's weights;
+            # M = 16: activations quantized straight into the skinny tile layout
             i = (p * 4 + s) % self.pool
-            F.quant_rows(t["xs"][s], q1, s1)
+            F.quant_rows_tiled(t["xs"][s], q1, s1)
             F.linear(q1, s1, t["w1"][i], out=t["h"], act="gelu_tanh")
-            F.quant_rows(t["h"], q2, s2)
+            F.quant_rows_tiled(t["h"], q2, s2)
             F.linear(q2, s2, t["w2"][i], out=t["out"], residual=t["res"])
 
     def dominant_call(self, p):

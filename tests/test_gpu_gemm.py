@@ -372,3 +372,36 @@ def test_skinny_tiled_contract(gpu):
     with pytest.raises(ValueError, match="before pack_skinny"):
         pack_glu(wt)
     assert pack_skinny(wt) is wt
+
+
+def _tile_rows_np(q, M, K):
+    """Tile layout of an [M, K] e4m3 activation (rows padded to 16, K to 128 with zeros)."""
+    mp = -(-M // 16) * 16
+    full = np.zeros((mp, K), np.uint8)
+    full[:M] = q
+    return _tile_layout_np(full, K)
+
+
+@pytest.mark.parametrize("M,N,K,act", [(16, 6144, 1536, "gelu_tanh"), (16, 1536, 6144, None), (50, 4096, 1024, None),
+                                       (1, 16, 128, None), (33, 48, 176, None), (16, 2048, 1536, "geglu"),
+                                       (64, 256, 2064, "gelu_tanh")])
+def test_tiled_activations(gpu, M, N, K, act):
+    # quant_rows_tiled writes quant_rows' bytes in the tile layout (zeros elsewhere), and
+    # linear on it is bit-identical to linear on the row-major activations, with row-major
+    # or tiled weights
+    from instinctflash_amd.kernels import fp8 as F, pack_glu, pack_skinny, quant_rows, quant_rows_tiled
+    glu = act in ("geglu", "swiglu")
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn((M, K), generator=g) * 3).to(torch.bfloat16).to(gpu)
+    qa, sa = quant_rows(x)
+    ta, ts = quant_rows_tiled(x)
+    assert torch.equal(ts.view(torch.int32), sa.view(torch.int32))
+    assert np.array_equal(_q(ta.q), _tile_rows_np(_q(qa), M, K))
+    _, _, fw, _ = _make(gpu, 1, N, K, seed=N, bias=True)
+    w = pack_glu(fw) if glu else fw
+    n_out = N // 2 if glu else N
+    res = torch.randn((M, n_out), generator=g).to(torch.bfloat16).to(gpu)
+    ref = F.linear(qa, sa, w, act=act, residual=res, out_dtype=torch.float32)
+    for weight in (w, pack_skinny(w)):
+        got = F.linear(ta, ts, weight, act=act, residual=res, out_dtype=torch.float32)
+        assert torch.equal(got.view(torch.int32), ref.view(torch.int32)), f"tiled A {M}x{N}x{K} {act}"
