@@ -89,6 +89,29 @@ def measure(wl, steps, warmup, kernel_launches=64):
     return dict(step_ms=ev_ms / steps, wall_step_ms=wall_ms / steps, kernel_ms=kern_ms)
 
 
+def measure_calls(wl, launches):
+    """p50 µs of every call of the path on its own (graph of back-to-back calls,
+    weights rotating as in the step), with TFLOP/s, GB/s and both roofline
+    fractions (the C4 qkv / o projections sit near the ridge point)."""
+    import torch
+    out = []
+    side = torch.cuda.Stream()
+    for c in wl.calls():
+        side.wait_stream(torch.cuda.current_stream())
+        g = capture(lambda i: c.fn(i), launches, side)
+        time_graph(g)
+        us = sorted(time_graph(g)[0] / launches * 1e3 for _ in range(5))[2]
+        w = c.work
+        shape = f"{w.M}x{w.N}x{w.K}" + (f" {w.act}" if w.act else "") if c.kind == "gemm" else f"{w[0]}x{w[1]}"
+        tf = c.flops / us / 1e6
+        gbs = c.bytes / us / 1e3
+        out.append({"call": c.name, "kind": c.kind, "shape": shape, "us_p50": round(us, 3),
+                    "tflops": round(tf, 2), "gbs": round(gbs, 1), "frac_mfma": round(tf / FP8_PEAK_TFLOPS, 4),
+                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        del g
+    return out
+
+
 def summarize(wl, m):
     step_s = m["step_ms"] * 1e-3
     d = wl.dominant_gemm
@@ -183,7 +206,22 @@ def cpu_baseline(min_seconds=10.0):
     dt /= units
     gemms = [Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True)]
     nbytes = 4 * (sum(x.bytes for x in gemms) + quant_bytes(M, D) + quant_bytes(M, FF))
+    # second line: the same unit with dequantize-then-fp32-matmul (MKL) in place of _scaled_mm
+    d1, d2 = q1.float() * s1[:, None], q2.float() * s2[:, None]
+    cpu_path.c2_unit_fp32(xs, d1, d2, res)
+    units32, t0 = 0, time.perf_counter()
+    while True:
+        cpu_path.c2_unit_fp32(xs, d1, d2, res)
+        units32 += 1
+        dt32 = time.perf_counter() - t0
+        if dt32 >= min_seconds / 2 or units32 >= 100000:
+            break
+    dt32 /= units32
     return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "dequant_fp32_matmul": {"value": round(nbytes / dt32 / 1e9, 4), "unit": "GB/s",
+                                    "seconds_per_unit": round(dt32, 6), "units_timed": units32,
+                                    "sample": "same C2 units: per-token quant, dequantize, fp32 matmul (MKL), "
+                                              "fp32 epilogue"},
             "kind": "port", "seconds_per_unit": round(dt, 4), "units_timed": units,
             "sample": f"{units} full C2 units (4 flow steps x [quant, 16x1536->6144 GELU, quant, 16x6144->1536 "
                       "+res]) via torch._scaled_mm (oneDNN) on the host CPU, reference GI decomposition",
@@ -249,6 +287,7 @@ def main():
         m = measure(wl, steps, args.warmup)
         results[key] = summarize(wl, m)
         results[key]["steps"] = steps
+        results[key]["calls"] = measure_calls(wl, 32 if wl.bound == "hbm" else 8)
         if key == args.config:
             head = (wl, m)
         del wl

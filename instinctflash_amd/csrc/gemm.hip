@@ -398,7 +398,6 @@ __device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
 }
 
-constexpr int kBigBN = 256;
 
 // LDS layout of a tile with KB-byte rows: 16-byte chunk `ch` of row `row` is
 // stored at chunk position ch ^ f(row). gfx950's LDS serves a ds_read_b128 16
@@ -481,19 +480,20 @@ __device__ __forceinline__ v4f quad(const v16f& v, int q) {
   return v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
 }
 
-template <int BM, int KB, int STAGES, int OCC, bool GLU, int FM, bool PIPE>
+template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM, bool PIPE>
 __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
                                                      const uint8_t* __restrict__ W, int64_t ldw, int64_t K,
                                                      TileMap tmap, Epi e, Partials part) {
   using S = Swz<KB>;
-  constexpr int kRows = kBigBN + BM;
+  constexpr int kRows = BN + BM;
   constexpr int kStage = kRows * KB;
   constexpr int kRowsPerDma = 1024 / KB;           // rows one DMA instruction fills
   constexpr int kWT = 32 * FM;                     // tokens per wave tile
   constexpr int kWM = BM / kWT;                    // waves along tokens (2 along weight rows)
   constexpr int kWaves = 2 * kWM;
   constexpr int kLoads = kRows / kRowsPerDma / kWaves;  // DMA instructions per wave per stage
-  constexpr int kFN = 4;                           // 32-row weight fragments per wave (128 rows)
+  constexpr int kFN = BN / 64;                     // 32-row weight fragments per wave (2 waves along BN)
+  static_assert(BN % 64 == 0 && BN >= 128 && BN <= 256, "weight tile");
   constexpr int kFM = FM;                          // 32-token fragments per wave
   constexpr int kHalves = KB / 64;                 // 32x32x64 K steps per stage
   static_assert(BM % kWT == 0 && kRows % (kWaves * kRowsPerDma) == 0, "tile");
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 
   int tm, tn, split;
   if (!map_tile(tmap, tm, tn, split)) return;
-  const int64_t n0 = static_cast<int64_t>(tn) * kBigBN;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
   // this workgroup's K stages: [kt0, kt0 + nk)
   const int kt0 = static_cast<int>(split * part.kstages);
@@ -535,10 +535,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       const int row = blk * kRowsPerDma + lrow;
       const int64_t k0 = static_cast<int64_t>(kt) * KB + ((lpos ^ S::f(row)) << 4);
       const uint8_t* p;
-      if (blk * kRowsPerDma < kBigBN) {  // wave-uniform
+      if (blk * kRowsPerDma < BN) {  // wave-uniform
         p = W + min(n0 + row, e.N - 1) * ldw + k0;
       } else {
-        p = A + min(m0 + (row - kBigBN), e.M - 1) * lda + k0;
+        p = A + min(m0 + (row - BN), e.M - 1) * lda + k0;
       }
       dma16(p, buf + i * 1024);
     }
@@ -561,12 +561,12 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       v8i af[kFM];
 #pragma unroll
       for (int j = 0; j < kFM; ++j) {
-        const int row = kBigBN + wm * kWT + j * 32 + frow;
+        const int row = BN + wm * kWT + j * 32 + frow;
         af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
 #pragma unroll
       for (int i = 0; i < kFN; ++i) {
-        const int row = wn * 128 + i * 32 + frow;
+        const int row = wn * (32 * kFN) + i * 32 + frow;
         const v8i wf = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
 #pragma unroll
         for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wf, af[j], acc[i][j]);
@@ -592,12 +592,12 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     auto load_frags = [&](const uint8_t* base, v8i (&wf)[kFN], v8i (&af)[kFM]) {
 #pragma unroll
       for (int j = 0; j < kFM; ++j) {
-        const int row = kBigBN + wm * kWT + j * 32 + frow;
+        const int row = BN + wm * kWT + j * 32 + frow;
         af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
 #pragma unroll
       for (int i = 0; i < kFN; ++i) {
-        const int row = wn * 128 + i * 32 + frow;
+        const int row = wn * (32 * kFN) + i * 32 + frow;
         wf[i] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
       }
     };
@@ -675,9 +675,9 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     asm volatile("" ::: "memory");
     __syncthreads();
     float* tile = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
-    const int64_t nw = n0 + wn * 128;
+    const int64_t nw = n0 + wn * (32 * kFN);
     const int64_t mw = m0 + wm * kWT;
-    const int col = (lane & 31) * 4;
+    const int col = (lane & 31) * 4;  // packed column of the wave tile (32 * kFN of them)
 #pragma unroll
     for (int j = 0; j < kFM; ++j) {
 #pragma unroll
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         for (int q = 0; q < 4; ++q)
           *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (nw + col < e.N) {
+      if (col < 32 * kFN && nw + col < e.N) {
 #pragma unroll 4
         for (int r = lane >> 5; r < 32; r += 2) {
           const int64_t m = mw + j * 32 + r;
@@ -709,16 +709,18 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   //     before its math. Every output row is written as one contiguous segment.
   // The barrier keeps the stage buffers alive until every wave is done with
   // its MFMAs and publishes the token scales.
-  constexpr int kCols = GLU ? 64 : 128;            // output columns of a wave tile
+  constexpr int kCols = GLU ? 16 * kFN : 32 * kFN;  // output columns of a wave tile
   constexpr int kLanesPerRow = kCols / 4;
   constexpr int kRowsPerPass = 64 / kLanesPerRow;
   constexpr int kRowIters = 32 / kRowsPerPass;
-  const int64_t nw = n0 + wn * 128;                // first (packed) weight row of the wave tile
+  static_assert(32 % kRowsPerPass == 0, "epilogue row passes");
+  const int64_t nw = n0 + wn * (32 * kFN);                // first (packed) weight row of the wave tile
   const int64_t mw = m0 + wm * kWT;                 // first token of the wave tile
   const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
   const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
   const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
-  const bool col_ok = c_out < (GLU ? e.N / 2 : e.N);
+  // lanes past kRowsPerPass whole rows (96-column tiles) have no column of their own
+  const bool col_ok = lane < kRowsPerPass * kLanesPerRow && c_out < (GLU ? e.N / 2 : e.N);
   const int64_t np = col_ok ? nw + pc : 0;         // packed weight row (any valid row if unused)
   const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
   const float4 sw0 = epi_sw4(e, np);
@@ -1112,10 +1114,10 @@ struct BigPlan {
   size_t ws_bytes;  // fp32 partials of all slices
 };
 
-__host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int kb) {
+__host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int bn, int kb) {
   BigPlan p{};
   p.tiles_m = (M + bm - 1) / bm;
-  p.tiles_n = (N + kBigBN - 1) / kBigBN;
+  p.tiles_n = (N + bn - 1) / bn;
   const int64_t tiles = p.tiles_m * p.tiles_n;
   const int64_t nk = K / kb;
   int64_t s = 1;
@@ -1130,10 +1132,10 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int kb
   return p;
 }
 
-template <int BM, int KB, int STAGES, int OCC, bool GLU, int FM = 2, bool PIPE = false>
+template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM = 2, bool PIPE = false>
 int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e,
                void* ws, size_t ws_bytes, hipStream_t st) {
-  const BigPlan p = big_plan(e.M, e.N, K, BM, KB);
+  const BigPlan p = big_plan(e.M, e.N, K, BM, BN, KB);
   if (p.tiles_m * p.tiles_n * p.ksplit > 0x7FFFFFF0LL) return IFX_ERR_UNSUPPORTED;
   Partials part{nullptr, e.N, p.kstages};
   if (p.ksplit > 1) {
@@ -1141,7 +1143,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
     part.base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);  // tickets stay untouched
   }
   const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
-  hipLaunchKernelGGL((gemm_big<BM, KB, STAGES, OCC, GLU, FM, PIPE>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
+  hipLaunchKernelGGL((gemm_big<BM, BN, KB, STAGES, OCC, GLU, FM, PIPE>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
                      0, st, a, lda, w, ldw, K, t, e, part);
   if (p.ksplit > 1) {
     const int64_t threads = e.M * ((GLU ? e.N / 2 : e.N) / 4);
@@ -1230,19 +1232,44 @@ constexpr int kBigKB = 128;
 
 inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; }
 
-// The wide tile unless it leaves fewer than 192 tiles.
-inline bool use_wide(int64_t M, int64_t N) { return ((M + 255) / 256) * ((N + 255) / 256) >= 192; }
+// Large-M configuration for a shape:
+//  * kWide / kWide192: 256 tokens x 256 (or 192) weight rows per workgroup, one
+//    workgroup per CU. 192-row tiles are taken (non-GLU only) when they need
+//    fewer tile rounds on the 256 CUs, weighted by tile height and efficiency:
+//    e.g. an 8192 x 3072 output is 384 tiles of 256 rows (a half-empty second
+//    round) but 512 tiles of 192 rows (two full rounds): 329 -> 302 us for
+//    K = 14336.
+//  * kNarrow: fewer than 192 tiles of 256 x 256 -- 128-token tiles, two
+//    workgroups per CU, plus split K.
+enum class BigCfg { kWide, kWide192, kNarrow };
+
+inline BigCfg pick_big(int64_t M, int64_t N, bool glu) {
+  const int64_t tm = (M + 255) / 256;
+  const int64_t t256 = tm * ((N + 255) / 256);
+  if (t256 < 192) return BigCfg::kNarrow;
+#ifndef IFX_EXP_NO192
+  if (!glu) {
+    const int64_t t192 = tm * ((N + 191) / 192);
+    // a 192-row tile does ~15% less work per unit time than a 256-row one
+    // (measured: 8192x9216x3072, 6 full rounds of 192 vs 4.5 of 256, is 2.5% slower)
+    if (((t192 + 255) / 256) * 192 * 115 < ((t256 + 255) / 256) * 256 * 100) return BigCfg::kWide192;
+  }
+#endif
+  return BigCfg::kWide;
+}
 
 template <bool GLU>
 int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e, void* ws,
                  size_t ws_bytes, hipStream_t st) {
-#ifdef IFX_EXP_BM
-  if (use_wide(e.M, e.N))
-    return launch_big<IFX_EXP_BM, IFX_EXP_KB, IFX_EXP_ST, IFX_EXP_OCC, GLU, IFX_EXP_FM, IFX_EXP_PIPE>(
-        a, lda, w, ldw, K, e, ws, ws_bytes, st);
-#endif
-  if (use_wide(e.M, e.N)) return launch_big<256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
-  return launch_big<128, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+  switch (pick_big(e.M, e.N, GLU)) {
+    case BigCfg::kWide192:
+      if constexpr (!GLU) return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      [[fallthrough]];
+    case BigCfg::kWide:
+      return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+    default:
+      return launch_big<128, 256, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+  }
 }
 
 }  // namespace
@@ -1256,7 +1283,11 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   if (M <= kSkinnyMaxM) return skinny_plan(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0).ws_bytes;
   if (!big_path(M, K)) return 0;
-  return use_wide(M, N) ? big_plan(M, N, K, 256, 128).ws_bytes : big_plan(M, N, K, 128, 64).ws_bytes;
+  switch (pick_big(M, N, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0)) {
+    case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
+    case BigCfg::kWide: return big_plan(M, N, K, 256, 256, 128).ws_bytes;
+    default: return big_plan(M, N, K, 128, 256, 64).ws_bytes;
+  }
 }
 
 }  // extern "C"

@@ -61,6 +61,22 @@ def quant_bytes(M: int, K: int) -> int:
 
 
 @dataclass
+class Call:
+    name: str
+    kind: str      # "gemm" or "quant"
+    work: object   # Gemm, or (M, K) of a quantizer pass
+    fn: object     # fn(i): run with weight set i % pool
+
+    @property
+    def flops(self) -> int:
+        return self.work.flops if self.kind == "gemm" else 0
+
+    @property
+    def bytes(self) -> int:
+        return self.work.bytes if self.kind == "gemm" else quant_bytes(*self.work)
+
+
+@dataclass
 class Workload:
     key: str
     title: str
@@ -90,15 +106,21 @@ class Workload:
         return self.gemm_bytes + self.quant_bytes
 
     def step(self):
-        self._run(self._i % self.pool)
+        """One timed unit: every call of the path, steps_per_unit times."""
+        for s in range(self.steps_per_unit):
+            i = self._i * self.steps_per_unit + s
+            for c in self.calls():
+                c.fn(i)
         self._i += 1
 
-    def _run(self, p: int):
+    def calls(self) -> list:
+        """The path's calls in order, as Call(name, kind, work, fn): fn(i) runs the
+        call with weight set i % pool; work is the Gemm or the quantizer's (M, K)."""
         raise NotImplementedError
 
-    def dominant_call(self, p: int):
+    def dominant_call(self, i: int):
         """Launch only the dominant kernel (its inputs prepared by an earlier step)."""
-        raise NotImplementedError
+        next(c for c in self.calls() if c.name == self.dominant).fn(i)
 
     @property
     def dominant_gemm(self) -> Gemm:
@@ -161,15 +183,14 @@ class C1(Workload):
         self.tensors = dict(x=xb, w=ws, qa=F.quant_rows_tiled(xb),
                             out=torch.empty((M, N), dtype=torch.bfloat16, device=dev))
 
-    def _run(self, p):
+    def calls(self):
         t = self.tensors
         qa, sa = t["qa"]
-        F.quant_rows_tiled(t["x"], qa, sa)  # M <= 64: activations in the skinny tile layout
-        F.linear(qa, sa, t["w"][p], out=t["out"])
-
-    def dominant_call(self, p):
-        t = self.tensors
-        F.linear(*t["qa"], t["w"][p % self.pool], out=t["out"])
+        g = self.gemms[0]
+        return [  # M <= 64: activations in the skinny tile layout
+            Call("quant x", "quant", (g.M, g.K), lambda i: F.quant_rows_tiled(t["x"], qa, sa)),
+            Call("up", "gemm", g, lambda i: F.linear(qa, sa, t["w"][i % self.pool], out=t["out"])),
+        ]
 
 
 # ---------------------------------------------------------------------------
@@ -196,22 +217,22 @@ class C2(Workload):
                             q2=F.quant_rows_tiled(h.zero_()), h=h,
                             out=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
 
-    def _run(self, p):
+    def calls(self):
+        # one flow step (the unit runs it 4 times, fresh x each time); one weight set
+        # per (unit, flow step): a deep DiT streams each layer's weights; M = 16:
+        # activations quantized straight into the skinny tile layout
         t = self.tensors
         q1, s1 = t["q1"]
         q2, s2 = t["q2"]
-        for s in range(4):
-            # one weight set per (step, flow step): a deep DiT streams each layer's weights;
-            # M = 16: activations quantized straight into the skinny tile layout
-            i = (p * 4 + s) % self.pool
-            F.quant_rows_tiled(t["xs"][s], q1, s1)
-            F.linear(q1, s1, t["w1"][i], out=t["h"], act="gelu_tanh")
-            F.quant_rows_tiled(t["h"], q2, s2)
-            F.linear(q2, s2, t["w2"][i], out=t["out"], residual=t["res"])
-
-    def dominant_call(self, p):
-        t = self.tensors
-        F.linear(*t["q1"], t["w1"][p % self.pool], out=t["h"], act="gelu_tanh")
+        up, down = self.gemms
+        return [
+            Call("quant x", "quant", (up.M, up.K), lambda i: F.quant_rows_tiled(t["xs"][i % 4], q1, s1)),
+            Call("up", "gemm", up,
+                 lambda i: F.linear(q1, s1, t["w1"][i % self.pool], out=t["h"], act="gelu_tanh")),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows_tiled(t["h"], q2, s2)),
+            Call("down", "gemm", down,
+                 lambda i: F.linear(q2, s2, t["w2"][i % self.pool], out=t["out"], residual=t["res"])),
+        ]
 
 
 # ---------------------------------------------------------------------------
@@ -235,18 +256,17 @@ class C3(Workload):
                             q2=b.q(M, FF), h=torch.empty((M, FF), dtype=torch.bfloat16, device=dev),
                             out=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
 
-    def _run(self, p):
+    def calls(self):
         t = self.tensors
         q1, s1 = t["q1"]
         q2, s2 = t["q2"]
-        F.quant_rows(t["x"], q1, s1)
-        F.linear(q1, s1, t["wgu"], out=t["h"], act="geglu")
-        F.quant_rows(t["h"], q2, s2)
-        F.linear(q2, s2, t["wd"], out=t["out"], residual=t["res"])
-
-    def dominant_call(self, p):
-        t = self.tensors
-        F.linear(*t["q1"], t["wgu"], out=t["h"], act="geglu")
+        gu, down = self.gemms
+        return [
+            Call("quant x", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["x"], q1, s1)),
+            Call("gate_up", "gemm", gu, lambda i: F.linear(q1, s1, t["wgu"], out=t["h"], act="geglu")),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], q2, s2)),
+            Call("down", "gemm", down, lambda i: F.linear(q2, s2, t["wd"], out=t["out"], residual=t["res"])),
+        ]
 
 
 # ---------------------------------------------------------------------------
@@ -286,22 +306,21 @@ class C4(Workload):
                             r1=torch.empty((M, D), dtype=torch.bfloat16, device=dev),
                             r2=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
 
-    def _run(self, p):
+    def calls(self):
         t = self.tensors
         q, s = t["q"]
         qh, sh = t["qh"]
-        F.quant_rows(t["xa"], q, s)
-        F.linear(q, s, t["wqkv"], out=t["qkv"])
-        F.quant_rows(t["xo"], q, s)
-        F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"])
-        F.quant_rows(t["xm"], q, s)
-        F.linear(q, s, t["wgu"], out=t["h"], act="swiglu")
-        F.quant_rows(t["h"], qh, sh)
-        F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"])
-
-    def dominant_call(self, p):
-        t = self.tensors
-        F.linear(*t["q"], t["wgu"], out=t["h"], act="swiglu")
+        qkv, o, gu, down = self.gemms
+        return [
+            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s)),
+            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"])),
+            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s)),
+            Call("o", "gemm", o, lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"])),
+            Call("quant mlp in", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["xm"], q, s)),
+            Call("gate_up", "gemm", gu, lambda i: F.linear(q, s, t["wgu"], out=t["h"], act="swiglu")),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh)),
+            Call("down", "gemm", down, lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"])),
+        ]
 
 
 # ---------------------------------------------------------------------------
@@ -336,22 +355,23 @@ class C5(Workload):
                             r1=torch.empty((M, D), dtype=torch.bfloat16, device=dev),
                             r2=torch.empty((M, D), dtype=torch.bfloat16, device=dev))
 
-    def _run(self, p):
+    def calls(self):
         t = self.tensors
         q, s = t["q"]
         qh, sh = t["qh"]
-        F.quant_rows(t["xa"], q, s)
-        F.linear(q, s, t["wqkv"], out=t["qkv"])
-        F.quant_rows(t["xo"], q, s)
-        F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"], gate=t["gate_o"])
-        F.quant_rows(t["xm"], q, s)
-        F.linear(q, s, t["wu"], out=t["h"], act="gelu_tanh")
-        F.quant_rows(t["h"], qh, sh)
-        F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"], gate=t["gate_f"])
-
-    def dominant_call(self, p):
-        t = self.tensors
-        F.linear(*t["q"], t["wu"], out=t["h"], act="gelu_tanh")
+        qkv, o, up, down = self.gemms
+        return [
+            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s)),
+            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"])),
+            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s)),
+            Call("o", "gemm", o,
+                 lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"], gate=t["gate_o"])),
+            Call("quant mlp in", "quant", (up.M, up.K), lambda i: F.quant_rows(t["xm"], q, s)),
+            Call("up", "gemm", up, lambda i: F.linear(q, s, t["wu"], out=t["h"], act="gelu_tanh")),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh)),
+            Call("down", "gemm", down,
+                 lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"], gate=t["gate_f"])),
+        ]
 
 
 CONFIGS = {"C1": C1, "C2": C2, "C3": C3, "C4": C4, "C5": C5}

@@ -55,3 +55,27 @@ def c2_unit(xs, w1, s1, w2, s2, res):
         q2, sa2 = quant_rows(h)
         out = linear(q2, sa2, w2, s2, residual=res)
     return out
+
+
+def linear_fp32(q, sa, wd, bias=None, act=None, residual=None):
+    """Dequantize-then-fp32-matmul (benchmarks/native/fp8_probe.py:36): wd is the
+    dequantized weight (q_w * s_w) in fp32; the activation is dequantized per row."""
+    y = (q.float() * sa[:, None]) @ wd.t()
+    if bias is not None:
+        y = y + bias
+    if act == "gelu_tanh":
+        y = Fn.gelu(y, approximate="tanh")
+    if residual is not None:
+        y = residual.float() + y
+    return y.to(torch.bfloat16)
+
+
+def c2_unit_fp32(xs, wd1, wd2, res):
+    """C2 unit with the dequantize-then-fp32-matmul CPU path (MKL)."""
+    out = None
+    for x in xs:
+        q, sa = quant_rows(x)
+        h = linear_fp32(q, sa, wd1, act="gelu_tanh")
+        q2, sa2 = quant_rows(h)
+        out = linear_fp32(q2, sa2, wd2, residual=res)
+    return out

@@ -405,3 +405,14 @@ def test_tiled_activations(gpu, M, N, K, act):
     for weight in (w, pack_skinny(w)):
         got = F.linear(ta, ts, weight, act=act, residual=res, out_dtype=torch.float32)
         assert torch.equal(got.view(torch.int32), ref.view(torch.int32)), f"tiled A {M}x{N}x{K} {act}"
+
+
+@pytest.mark.parametrize("M,N,K,act,resgate", [(4096, 3072, 640, "gelu_tanh", False), (4000, 3008, 512, None, True),
+                                               (4096, 3072, 384, None, False)])
+def test_wide_192_row_tiles(gpu, oracle_mod, M, N, K, act, resgate):
+    # output shapes whose 256-row tiles would leave a partial round on 256 CUs take
+    # 192-row weight tiles; ragged N ends inside a tile
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
+    res = torch.randn((M, N), generator=g).to(torch.bfloat16) if resgate else None
+    gate = torch.rand(N, generator=g).to(torch.bfloat16) if resgate else None
+    _check(gpu, oracle_mod, qa, sa, fw, f"wide192 {M}x{N}x{K}", act=act, residual=res, gate=gate)
