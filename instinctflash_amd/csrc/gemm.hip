@@ -1239,14 +1239,19 @@ inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; 
 //    e.g. an 8192 x 3072 output is 384 tiles of 256 rows (a half-empty second
 //    round) but 512 tiles of 192 rows (two full rounds): 329 -> 302 us for
 //    K = 14336.
-//  * kNarrow: fewer than 192 tiles of 256 x 256 -- 128-token tiles, two
-//    workgroups per CU, plus split K.
-enum class BigCfg { kWide, kWide192, kNarrow };
+//  * kSmall: fewer than 192 tiles of 256 x 256 and K <= 4096 -- 64 tokens x
+//    128 weight rows, 2 waves, four workgroups per CU, usually no split (e.g.
+//    1024 x 2560 x 2048: 28 -> 18 us against split-K narrow tiles, whose fp32
+//    partials cost more than the short K loop);
+//  * kNarrow: fewer than 192 tiles and a longer K -- 128-token tiles, two
+//    workgroups per CU, plus split K (1024 x 2048 x 11008: 51 us, against 67 us
+//    for small tiles without a split).
+enum class BigCfg { kWide, kWide192, kSmall, kNarrow };
 
-inline BigCfg pick_big(int64_t M, int64_t N, bool glu) {
+inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
   const int64_t tm = (M + 255) / 256;
   const int64_t t256 = tm * ((N + 255) / 256);
-  if (t256 < 192) return BigCfg::kNarrow;
+  if (t256 < 192) return K <= 4096 ? BigCfg::kSmall : BigCfg::kNarrow;
 #ifndef IFX_EXP_NO192
   if (!glu) {
     const int64_t t192 = tm * ((N + 191) / 192);
@@ -1261,12 +1266,14 @@ inline BigCfg pick_big(int64_t M, int64_t N, bool glu) {
 template <bool GLU>
 int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e, void* ws,
                  size_t ws_bytes, hipStream_t st) {
-  switch (pick_big(e.M, e.N, GLU)) {
+  switch (pick_big(e.M, e.N, K, GLU)) {
     case BigCfg::kWide192:
       if constexpr (!GLU) return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       [[fallthrough]];
     case BigCfg::kWide:
       return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+    case BigCfg::kSmall:
+      return launch_big<64, 128, 64, 2, 4, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     default:
       return launch_big<128, 256, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
@@ -1283,9 +1290,10 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   if (M <= kSkinnyMaxM) return skinny_plan(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0).ws_bytes;
   if (!big_path(M, K)) return 0;
-  switch (pick_big(M, N, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0)) {
+  switch (pick_big(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0)) {
     case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
     case BigCfg::kWide: return big_plan(M, N, K, 256, 256, 128).ws_bytes;
+    case BigCfg::kSmall: return big_plan(M, N, K, 64, 128, 64).ws_bytes;
     default: return big_plan(M, N, K, 128, 256, 64).ws_bytes;
   }
 }

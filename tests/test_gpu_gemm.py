@@ -231,7 +231,7 @@ def test_workspace_reuse_across_shapes(gpu, oracle_mod):
         _assert_close(_f(out), _ref(oracle_mod, qa, sa, fw), f"seq {i}: {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K,act", [(816, 2048, 16384, None), (1024, 2560, 2048, None), (300, 1024, 4096, "swiglu"),
+@pytest.mark.parametrize("M,N,K,act", [(816, 2048, 16384, None), (512, 1024, 2048, None), (300, 1024, 4096, "swiglu"),
                                        (1024, 2048, 11008, None), (257, 512, 2048, "gelu_tanh")])
 def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
     # few output tiles: the large-M kernel splits K and a reduce kernel applies the epilogue
