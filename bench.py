@@ -139,14 +139,17 @@ def summarize(wl, m):
 
 
 def measure_producers(dev, launches=32):
-    """The pre-norm producer (residual update + LayerNorm + adaLN + per-token
-    quant) at the C5 and C2 shapes: µs per call (graph of back-to-back calls,
+    """The row kernels around the projections: the pre-norm producer (residual
+    update + LayerNorm + adaLN + per-token quant) at the C5 and C2 shapes and the
+    QKV split consumer at the C4 shape: µs per call (graph of back-to-back calls,
     median of 5) and GB/s of algorithmic bytes against the 8 TB/s roofline."""
     import torch
-    from instinctflash_amd.workloads import PRODUCERS, NormQuant
+    from instinctflash_amd.workloads import CONSUMERS, PRODUCERS, NormQuant
     res = {}
-    for key, (M, D) in PRODUCERS.items():
-        p = NormQuant(dev, M, D)
+    jobs = [(f"residual_norm_quant {key}", lambda M=M, D=D: NormQuant(dev, M, D)) for key, (M, D) in PRODUCERS.items()]
+    jobs += [(f"qkv_split {key}", lambda cls=cls: cls(dev)) for key, cls in CONSUMERS.items()]
+    for key, make in jobs:
+        p = make()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -159,7 +162,7 @@ def measure_producers(dev, launches=32):
         gbs = p.bytes / us / 1e3
         res[key] = {"kernel": p.title, "us": round(us, 3), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                     "bytes": p.bytes}
-        _log(f"[bench] producer {key}: {p.title}: {us:.2f} us, {gbs:.0f} GB/s")
+        _log(f"[bench] {key}: {p.title}: {us:.2f} us, {gbs:.0f} GB/s")
     return res
 
 

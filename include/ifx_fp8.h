@@ -46,6 +46,7 @@ extern "C" {
 /* source dtypes for the quantizers */
 #define IFX_DTYPE_BF16 0
 #define IFX_DTYPE_F32 1
+#define IFX_DTYPE_F16 2 /* outputs of ifx_qkv_split only */
 
 /* activation selector for gated_act_quant (reference kernels/activation.py:15-16) */
 #define IFX_ACT_GELU_TANH 0
@@ -204,6 +205,25 @@ int ifx_residual_norm_quant(void* res, int res_dtype, int64_t ldres, const void*
                             const float* mod_shift, const int32_t* mod_index, int flags, float eps, void* q,
                             int64_t ldq, float* q_scale, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t D,
                             void* stream);
+
+/*
+ * Split a fused QKV accumulator qkv [T, (HQ + 2*HKV) * HD] (BF16 or F32, row
+ * stride ldqkv) into Q, K, V heads:
+ *   x = qkv * row[t] * col + bias            (row [T], col/bias [(HQ+2HKV)*HD] f32; each may be NULL)
+ *   Q, K heads: x = x / sqrt(mean(x^2) + eps) * q_norm|k_norm  (per head; both NULL or both [HD])
+ *   Q, K heads: rotary on pairs (i, i + HD/2), angle = pos[t * ldpos + sections[i]] * inv_freq[i]
+ *               (f32 pos table, int32 sections [HD/2] or NULL = column 0; inv_freq [HD/2] or NULL = none)
+ *   store Q at q_out[t*sq_t + h*sq_h + d], K / V at k_out / v_out[(kv_base + t)*s*_t + h*s*_h + d]
+ * out_dtype: IFX_DTYPE_BF16, IFX_DTYPE_F16 or IFX_DTYPE_F32 for all three;
+ * kv_base_dev: NULL, or a device int32 read in place of kv_base. HD even, <= 256.
+ * Replaces: instinctflash/kernels/rope.py:89-116 `qkv_split` (kernel :21-80).
+ */
+int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* row, const float* col,
+                  const float* bias, const float* q_norm, const float* k_norm, float eps, const float* inv_freq,
+                  const float* pos, int64_t ldpos, const int32_t* sections, void* q_out, int64_t sq_t,
+                  int64_t sq_h, void* k_out, int64_t sk_t, int64_t sk_h, void* v_out, int64_t sv_t, int64_t sv_h,
+                  int out_dtype, int64_t kv_base, const int32_t* kv_base_dev, int64_t T, int64_t HQ, int64_t HKV,
+                  int64_t HD, void* stream);
 
 /* Activation scaling of ifx_quant_linear. */
 #define IFX_SCALE_ROW 0    /* one scale per token (row) */

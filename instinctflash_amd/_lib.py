@@ -25,6 +25,7 @@ ERR_UNSUPPORTED = -4
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+DTYPE_F16 = 2
 
 ACT_GELU_TANH = 0
 ACT_SILU = 1
@@ -66,6 +67,8 @@ SIGNATURES = {
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
     "ifx_fp8_skinny_tiled_bytes": (_SZ, [_I64, _I64]),
+    "ifx_qkv_split": (_INT, [_P, _INT, _I64, _P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _I64,
+                             _P, _I64, _I64, _P, _I64, _I64, _INT, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "ifx_quant_rows_tiled_bytes": (_SZ, [_I64, _I64]),
     "ifx_quant_rows_tiled": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P]),
     "ifx_fp8_pack_skinny": (_INT, [_P, _I64, _I64, _I64, _P, _P]),

@@ -410,4 +410,39 @@ class NormQuant:
                                    q=self.q, q_scale=self.qs)
 
 
+class QkvSplit:
+    """``qkv_split`` after the C4 qkv projection (Qwen2.5-style: 16 query / 2 KV
+    heads of 128, bias, M-RoPE with 3 position sections), writing q and the K/V
+    cache rows. Algorithmic bytes: the bf16 accumulator read once, q/k/v written
+    once (bf16), the scale/bias vectors and position rows once."""
+
+    def __init__(self, dev, T=1024, HQ=16, HKV=2, HD=128, seed=0):
+        from .kernels import rope as R
+        self.R, self.T, self.HQ, self.HKV, self.HD = R, T, HQ, HKV, HD
+        g = _gen(seed)
+        C = (HQ + 2 * HKV) * HD
+        self.raw = torch.randn(T, C, generator=g).to(torch.bfloat16).to(dev)
+        self.row = (torch.rand(T, generator=g) + 0.5).to(dev)
+        self.col = (torch.rand(C, generator=g) + 0.5).to(dev)
+        self.bias = torch.randn(C, generator=g).to(dev)
+        self.inv = R.rope_inv_freq(HD, 1e6, dev)
+        self.pos = torch.stack([torch.arange(T)] * 3, 1).float().to(dev)
+        self.sec = (torch.arange(HD // 2) % 3).int().to(dev)
+        self.q = torch.empty(T, HQ, HD, dtype=torch.bfloat16, device=dev)
+        self.kc = torch.empty(2 * T, HKV, HD, dtype=torch.bfloat16, device=dev)
+        self.vc = torch.empty_like(self.kc)
+        self.title = f"qkv_split {T} tokens, {HQ}+2x{HKV} heads x {HD} (rescale, bias, M-RoPE, KV-cache store)"
+
+    @property
+    def bytes(self) -> int:
+        C = (self.HQ + 2 * self.HKV) * self.HD
+        return 2 * self.T * C * 2 + 2 * C * 4 + self.T * (4 + 3 * 4) + self.HD // 2 * (4 + 4)
+
+    def step(self, i=0):
+        self.R.qkv_split(self.raw, self.q, self.kc, self.vc, heads_q=self.HQ, heads_kv=self.HKV, head_dim=self.HD,
+                         row=self.row, col=self.col, bias=self.bias, inv_freq=self.inv, pos=self.pos,
+                         sections=self.sec, kv_base=self.T // 2)
+
+
 PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}
+CONSUMERS = {"C4": QkvSplit}

@@ -24,6 +24,11 @@ Parts
     b)*gate to 1e-4, and the rsqrt-normalized row), by closed forms (a constant
     row normalizes to +-1 / 0, unit-RMS rows are fixed points of RMS norm) and by
     torch.nn.functional.layer_norm / rms_norm.
+  * qkv_split: the QKV split of kernels/rope.py:21-80 (rescale, per-head q/k
+    RMSNorm, rotary with float32 angles). Pinned by the reference's own test
+    expectation (tests/test_gi_kernels.py:58-90) evaluated with torch, by the
+    rotation invariants (pair norms preserved, position 0 = identity, angle
+    additivity) and by unit RMS of normalized heads.
 """
 from __future__ import annotations
 
@@ -255,3 +260,40 @@ def residual_norm(res, delta=None, delta_row=None, delta_col=None, bias=None, ga
     if mod_scale is not None:
         y = y * (1.0 + rows_of(mod_scale).astype(np.float64)) + rows_of(mod_shift).astype(np.float64)
     return x, y
+
+
+def qkv_split(qkv, HQ, HKV, HD, row=None, col=None, bias=None, inv_freq=None, pos=None, sections=None,
+              q_norm=None, k_norm=None, eps=1e-6):
+    """QKV split of instinctflash/kernels/rope.py:21-80, restated.
+
+    Rescale in float32 in the reference's order (x*row, *col, +bias); per-head
+    RMSNorm of Q and K in float64 (x / sqrt(mean(x^2) + eps) * w); rotary with
+    the reference's float32 angle pos[t, section[i]] * inv_freq[i] (:60-64) and
+    float64 cos/sin, split-half pairing (i, i + HD/2). Returns float64
+    (q [T, HQ, HD], k [T, HKV, HD], v [T, HKV, HD])."""
+    f32 = np.float32
+    x = np.asarray(qkv, dtype=f32)
+    T = x.shape[0]
+    if row is not None:
+        x = (x * np.asarray(row, f32)[:, None]).astype(f32)
+    if col is not None:
+        x = (x * np.asarray(col, f32)[None, :]).astype(f32)
+    if bias is not None:
+        x = (x + np.asarray(bias, f32)[None, :]).astype(f32)
+    x = x.astype(np.float64).reshape(T, HQ + 2 * HKV, HD)
+    qk = x[:, :HQ + HKV]
+    if q_norm is not None:
+        rs = 1.0 / np.sqrt((qk * qk).mean(axis=2, keepdims=True) + float(f32(eps)))
+        w = np.concatenate([np.broadcast_to(np.asarray(q_norm, np.float64), (HQ, HD)),
+                            np.broadcast_to(np.asarray(k_norm, np.float64), (HKV, HD))])
+        qk = qk * rs * w[None]
+    if inv_freq is not None:
+        half = HD // 2
+        sec = np.zeros(half, np.int64) if sections is None else np.asarray(sections, np.int64)
+        p = np.asarray(pos, f32)[:, sec]                                   # [T, half]
+        ang = (p * np.asarray(inv_freq, f32)[None, :]).astype(f32).astype(np.float64)
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        lo, hi = qk[..., :half], qk[..., half:]
+        qk = np.concatenate([lo * c - hi * s, hi * c + lo * s], axis=2)
+    v = x[:, HQ + HKV:]
+    return qk[:, :HQ], qk[:, HQ:], v

@@ -352,3 +352,67 @@ def test_residual_norm_tables_and_bf16_store(oracle_mod):
     # bf16 residual: the stored (rounded) sum is what gets normalized
     xb, _ = oracle_mod.residual_norm(res, delta, res_bf16=True)
     assert np.array_equal(xb, oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16((res + delta).astype(np.float32))))
+
+
+# ---------------------------------------------------------------------------
+# qkv_split (kernels/rope.py:21-80)
+# ---------------------------------------------------------------------------
+
+def _qkv_case(T=7, HQ=4, HKV=2, HD=128, seed=2):
+    # the reference test's case (tests/test_gi_kernels.py:58-70), on the CPU
+    from instinctflash_amd.kernels.rope import rope_inv_freq
+    g = torch.Generator().manual_seed(seed)
+    raw = torch.randn(T, (HQ + 2 * HKV) * HD, generator=g).to(torch.bfloat16)
+    row = torch.rand(T, generator=g) + 0.5
+    col = torch.rand(raw.shape[1], generator=g) + 0.5
+    bias = torch.randn(raw.shape[1], generator=g)
+    qn, kn = torch.rand(HD, generator=g) + 0.5, torch.rand(HD, generator=g) + 0.5
+    inv = rope_inv_freq(HD, 1e6, "cpu")
+    pos = torch.stack([torch.arange(T), torch.arange(T) * 2, torch.arange(T) * 3], 1).float()
+    sec = (torch.arange(HD // 2) % 3).int()
+    return raw, row, col, bias, qn, kn, inv, pos, sec
+
+
+def test_qkv_split_matches_reference_test_expectation(oracle_mod):
+    T, HQ, HKV, HD = 7, 4, 2, 128
+    raw, row, col, bias, qn, kn, inv, pos, sec = _qkv_case()
+    q, k, v = oracle_mod.qkv_split(raw.float().numpy(), HQ, HKV, HD, row.numpy(), col.numpy(), bias.numpy(),
+                                   inv.numpy(), pos.numpy(), sec.numpy(), qn.numpy(), kn.numpy())
+    # the reference test's own formula (tests/test_gi_kernels.py:74-88), in torch float32
+    x = raw.float() * row[:, None] * col + bias
+    xq, xk, xv = x[:, :HQ * HD].view(T, HQ, HD), x[:, HQ * HD:(HQ + HKV) * HD].view(T, HKV, HD), \
+        x[:, (HQ + HKV) * HD:].view(T, HKV, HD)
+    rms = lambda t, w: t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6) * w  # noqa: E731
+    ang = pos.gather(1, sec.long()[None].expand(T, -1)) * inv
+
+    def rope(t):
+        c, s = ang.cos()[:, None], ang.sin()[:, None]
+        lo, hi = t[..., :HD // 2], t[..., HD // 2:]
+        return torch.cat([lo * c - hi * s, hi * c + lo * s], -1)
+    assert np.abs(q - rope(rms(xq, qn)).double().numpy()).max() < 1e-4
+    assert np.abs(k - rope(rms(xk, kn)).double().numpy()).max() < 1e-4
+    assert np.array_equal(v, xv.double().numpy())
+
+
+def test_qkv_split_invariants(oracle_mod):
+    from instinctflash_amd.kernels.rope import rope_inv_freq
+    T, HQ, HKV, HD = 5, 2, 1, 64
+    rng = np.random.default_rng(4)
+    raw = rng.standard_normal((T, (HQ + 2 * HKV) * HD)).astype(np.float32)
+    inv = rope_inv_freq(HD, 1e4, "cpu").numpy()
+    assert inv[0] == 1.0 and np.allclose(inv[1:] / inv[:-1], 1e4 ** (-2 / HD))
+    pos = (np.arange(T, dtype=np.float32) * 37)[:, None]
+    q0, k0, v0 = oracle_mod.qkv_split(raw, HQ, HKV, HD)
+    q, k, v = oracle_mod.qkv_split(raw, HQ, HKV, HD, inv_freq=inv, pos=pos)
+    half = HD // 2
+    pair = lambda t: t[..., :half] ** 2 + t[..., half:] ** 2  # noqa: E731
+    assert np.allclose(pair(q), pair(q0)) and np.allclose(pair(k), pair(k0))  # rotations keep pair norms
+    assert np.array_equal(q[0], q0[0]) and np.array_equal(v, v0)              # position 0: identity
+    # rotating by a then b equals rotating by a + b (float32 angles exact for these integers)
+    q2, _, _ = oracle_mod.qkv_split(np.concatenate([q[:, :, :].reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], 1)
+                                    .astype(np.float32), HQ, HKV, HD, inv_freq=inv, pos=pos)
+    qa, _, _ = oracle_mod.qkv_split(raw, HQ, HKV, HD, inv_freq=inv, pos=2 * pos)
+    assert np.abs(q2 - qa).max() < 1e-5
+    # normalized heads have unit RMS (unit weights)
+    qn, kn, _ = oracle_mod.qkv_split(raw, HQ, HKV, HD, q_norm=np.ones(HD), k_norm=np.ones(HD), eps=0.0)
+    assert np.allclose(np.sqrt((qn ** 2).mean(-1)), 1.0) and np.allclose(np.sqrt((kn ** 2).mean(-1)), 1.0)
