@@ -147,7 +147,7 @@ def measure_producers(dev, launches=32):
     from instinctflash_amd.workloads import CONSUMERS, PRODUCERS, NormQuant
     res = {}
     jobs = [(f"residual_norm_quant {key}", lambda M=M, D=D: NormQuant(dev, M, D)) for key, (M, D) in PRODUCERS.items()]
-    jobs += [(f"qkv_split {key}", lambda cls=cls: cls(dev)) for key, cls in CONSUMERS.items()]
+    jobs += [(f"{cls.__name__} {key}", lambda cls=cls: cls(dev)) for key, cls in CONSUMERS.items()]
     for key, make in jobs:
         p = make()
         side = torch.cuda.Stream()

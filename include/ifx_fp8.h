@@ -225,6 +225,25 @@ int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* ro
                   int out_dtype, int64_t kv_base, const int32_t* kv_base_dev, int64_t T, int64_t HQ, int64_t HKV,
                   int64_t HD, void* stream);
 
+/*
+ * Wan DiT QKV consumer: raw [rows, parts * D] (BF16 or F32, D = heads * head_dim,
+ * parts = 1 + (k_pool != NULL) + (v_pool != NULL): Q, then K, then V columns):
+ *   x = raw * row[r] * col + bias               (per part, columns of that part)
+ *   Q / K: x = x / sqrt(mean(x^2) + eps) * q_norm|k_norm   (over the full D; skipped if NULL)
+ *   Q / K: rotary on adjacent pairs (2j, 2j+1) of every head,
+ *          angle = pos[t * ldpos + sections[j]] * inv_freq[j] (j < head_dim/2; inv_freq NULL = none)
+ *   store Q at q_out[r * sq + c]; K / V at pool[b * s_b + slot * s_s + c], slot = slots[t] (or t)
+ * with t = r % tokens, b = r / tokens. As in the reference launch, part 1 is K:
+ * a V pool without a K pool is not written. head_dim % 8 == 0, <= 256; D <= 16384;
+ * 16-byte aligned bases and strides that are multiples of 8 elements.
+ * Replaces: instinctflash/kernels/wan.py:84-116 `wan_qkv` (kernel :19-81).
+ */
+int ifx_wan_qkv(const void* raw, int raw_dtype, int64_t ldraw, const float* row, const float* col,
+                const float* bias, const float* q_norm, const float* k_norm, float eps, const float* inv_freq,
+                const float* pos, int64_t ldpos, const int32_t* sections, void* q_out, int64_t sq, void* k_pool,
+                int64_t sk_b, int64_t sk_s, void* v_pool, int64_t sv_b, int64_t sv_s, const int32_t* slots,
+                int out_dtype, int64_t rows, int64_t tokens, int64_t heads, int64_t head_dim, void* stream);
+
 /* Activation scaling of ifx_quant_linear. */
 #define IFX_SCALE_ROW 0    /* one scale per token (row) */
 #define IFX_SCALE_TENSOR 1 /* one scale for the whole [M, K] activation */

@@ -67,6 +67,8 @@ SIGNATURES = {
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
     "ifx_fp8_skinny_tiled_bytes": (_SZ, [_I64, _I64]),
+    "ifx_wan_qkv": (_INT, [_P, _INT, _I64, _P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _P, _I64,
+                           _I64, _P, _I64, _I64, _P, _INT, _I64, _I64, _I64, _I64, _P]),
     "ifx_qkv_split": (_INT, [_P, _INT, _I64, _P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _INT, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "ifx_quant_rows_tiled_bytes": (_SZ, [_I64, _I64]),

@@ -57,13 +57,49 @@ __device__ __forceinline__ float load_in(const QkvArgs& a, int64_t idx) {
   return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(a.qkv)[idx]) << 16);
 }
 
-__device__ __forceinline__ void store_out(const QkvArgs& a, void* base, int64_t idx, float v) {
-  if (a.out_dtype == IFX_DTYPE_F32) {
+__device__ __forceinline__ void store_out(int out_dtype, void* base, int64_t idx, float v) {
+  if (out_dtype == IFX_DTYPE_F32) {
     static_cast<float*>(base)[idx] = v;
-  } else if (a.out_dtype == IFX_DTYPE_F16) {
+  } else if (out_dtype == IFX_DTYPE_F16) {
     static_cast<_Float16*>(base)[idx] = static_cast<_Float16>(v);
   } else {
     static_cast<__bf16*>(base)[idx] = static_cast<__bf16>(v);
+  }
+}
+
+// Eight consecutive values at a 16-byte aligned element index.
+__device__ __forceinline__ void load8(const void* base, bool f32, int64_t idx, float* v) {
+  if (f32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+}
+
+__device__ __forceinline__ void load8_f32(const float* p, float* v) { load8(p, true, 0, v); }
+
+__device__ __forceinline__ void store8(int out_dtype, void* base, int64_t idx, const float* v) {
+  if (out_dtype == IFX_DTYPE_F32) {
+    float* p = static_cast<float*>(base) + idx;
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else if (out_dtype == IFX_DTYPE_F16) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(v[i]);
+    *reinterpret_cast<h8*>(static_cast<_Float16*>(base) + idx) = h;
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + idx) =
+        make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
   }
 }
 
@@ -160,9 +196,137 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_split_kernel(QkvArgs 
     for (int j = 0; j < NJ; ++j) {
       if (!on[j]) continue;
       const int64_t i = lane + 64 * j;
-      store_out(a, dst, off + i, lo[j]);
-      store_out(a, dst, off + half + i, hi[j]);
+      store_out(a.out_dtype, dst, off + i, lo[j]);
+      store_out(a.out_dtype, dst, off + half + i, hi[j]);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wan DiT QKV consumer (reference instinctflash/kernels/wan.py:19-116): parts
+// Q | K | V of a raw accumulator row, each H*HD wide. Q and K are RMS-normalized
+// over their full width (before the head split) and rotated on adjacent channel
+// pairs (2j, 2j+1) of every head by pos[t, section[j]] * inv_freq[j]; Q is stored
+// densely, K / V into per-batch pools at row slots[t] (t = row % tokens).
+// One 256-lane workgroup per (row, part); 8-element groups per lane (4 pairs);
+// the row's HD/2 cos/sin values are computed once into LDS.
+// ---------------------------------------------------------------------------
+
+struct WanArgs {
+  const void* raw;
+  int64_t ldraw;
+  const float* row;
+  const float* col;
+  const float* bias;
+  const float* qnw;
+  const float* knw;
+  float eps;
+  const float* inv_freq;
+  const float* pos;
+  int64_t ldpos;
+  const int32_t* sections;
+  void* q;
+  int64_t sq;
+  void* kp;
+  int64_t sk_b, sk_s;
+  void* vp;
+  int64_t sv_b, sv_s;
+  const int32_t* slots;
+  int64_t tokens, D, HD;
+  int has_k, has_v;
+  int in_f32;
+  int out_dtype;
+};
+
+template <int VPT>
+__global__ __launch_bounds__(256) void wan_qkv_kernel(WanArgs a) {
+  __shared__ float red[4];
+  __shared__ float cs[128], sn[128];
+  const int64_t row = blockIdx.x;
+  const int part = blockIdx.y;  // 0 = Q, 1 = K, 2 = V
+  if ((part == 1 && !a.has_k) || (part == 2 && !a.has_v)) return;  // block-uniform
+  const int64_t b = row / a.tokens, t = row - b * a.tokens;
+  const int64_t D = a.D, half = a.HD / 2;
+  const bool rope = a.inv_freq != nullptr && part < 2;
+  const float* nw = part == 0 ? a.qnw : (part == 1 ? a.knw : nullptr);
+  if (rope) {
+    for (int64_t j = threadIdx.x; j < half; j += 256) {
+      const int64_t sec = a.sections ? a.sections[j] : 0;
+      sincosf(a.pos[t * a.ldpos + sec] * a.inv_freq[j], &sn[j], &cs[j]);
+    }
+  }
+  const int64_t col0 = part * D;
+  const float r = a.row ? a.row[row] : 1.0f;
+  float x[VPT][8];
+  bool on[VPT];
+  float ss = 0.0f;
+#pragma unroll
+  for (int jv = 0; jv < VPT; ++jv) {
+    const int64_t c = (static_cast<int64_t>(jv) * 256 + threadIdx.x) * 8;
+    on[jv] = c < D;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[jv][e] = 0.0f;
+    if (!on[jv]) continue;
+    load8(a.raw, a.in_f32 != 0, row * a.ldraw + col0 + c, x[jv]);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[jv][e] = x[jv][e] * r;
+    if (a.col) {
+      load8_f32(a.col + col0 + c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[jv][e] = x[jv][e] * v[e];
+    }
+    if (a.bias) {
+      load8_f32(a.bias + col0 + c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[jv][e] = x[jv][e] + v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = ss + x[jv][e] * x[jv][e];
+  }
+  if (nw) {  // block-uniform
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = red[0] + red[1] + red[2] + red[3];
+    const float rs = 1.0f / __builtin_sqrtf(tot / static_cast<float>(D) + a.eps);
+#pragma unroll
+    for (int jv = 0; jv < VPT; ++jv) {
+      if (!on[jv]) continue;
+      const int64_t c = (static_cast<int64_t>(jv) * 256 + threadIdx.x) * 8;
+      float w[8];
+      load8_f32(nw + c, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[jv][e] = x[jv][e] * rs * w[e];
+    }
+  }
+  if (rope) __syncthreads();  // the cos/sin table is complete
+  void* dst;
+  int64_t base;
+  if (part == 0) {
+    dst = a.q;
+    base = row * a.sq;
+  } else {
+    const int64_t slot = a.slots ? static_cast<int64_t>(a.slots[t]) : t;
+    dst = part == 1 ? a.kp : a.vp;
+    base = part == 1 ? b * a.sk_b + slot * a.sk_s : b * a.sv_b + slot * a.sv_s;
+  }
+#pragma unroll
+  for (int jv = 0; jv < VPT; ++jv) {
+    if (!on[jv]) continue;
+    const int64_t c = (static_cast<int64_t>(jv) * 256 + threadIdx.x) * 8;
+    if (rope) {
+      const int64_t j0 = (c % a.HD) / 2;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float ev = x[jv][2 * p], od = x[jv][2 * p + 1];
+        const float cc = cs[j0 + p], s = sn[j0 + p];
+        x[jv][2 * p] = ev * cc - od * s;
+        x[jv][2 * p + 1] = ev * s + od * cc;
+      }
+    }
+    store8(a.out_dtype, dst, base + c, x[jv]);
   }
 }
 
@@ -203,3 +367,41 @@ int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* ro
 }
 
 }  // extern "C"
+
+extern "C" int ifx_wan_qkv(const void* raw, int raw_dtype, int64_t ldraw, const float* row, const float* col,
+                           const float* bias, const float* q_norm, const float* k_norm, float eps,
+                           const float* inv_freq, const float* pos, int64_t ldpos, const int32_t* sections,
+                           void* q_out, int64_t sq, void* k_pool, int64_t sk_b, int64_t sk_s, void* v_pool,
+                           int64_t sv_b, int64_t sv_s, const int32_t* slots, int out_dtype, int64_t rows,
+                           int64_t tokens, int64_t heads, int64_t head_dim, void* stream) {
+  if (raw_dtype != IFX_DTYPE_BF16 && raw_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
+  if (out_dtype != IFX_DTYPE_BF16 && out_dtype != IFX_DTYPE_F32 && out_dtype != IFX_DTYPE_F16) return IFX_ERR_INVALID;
+  if (rows < 0 || tokens <= 0 || heads <= 0 || head_dim <= 0 || head_dim % 8 != 0) return IFX_ERR_INVALID;
+  if (head_dim > 256) return IFX_ERR_UNSUPPORTED;
+  const int64_t D = heads * head_dim;
+  if (D > 256 * 8 * 8) return IFX_ERR_UNSUPPORTED;
+  const int parts = 1 + (k_pool != nullptr) + (v_pool != nullptr);
+  if (ldraw < parts * D || sq < D) return IFX_ERR_INVALID;
+  if (inv_freq && (!pos || ldpos < 1)) return IFX_ERR_INVALID;
+  if (!(eps >= 0.0f)) return IFX_ERR_INVALID;
+  if (rows == 0) return IFX_OK;
+  if (!raw || !q_out) return IFX_ERR_INVALID;
+  // 16-byte groups of 8 elements: aligned bases, strides in multiples of 8
+  auto al = [](const void* p) { return p == nullptr || aligned16(p); };
+  if (!aligned16(raw) || !aligned16(q_out) || !al(k_pool) || !al(v_pool) || !al(col) || !al(bias) || !al(q_norm) ||
+      !al(k_norm) || ldraw % 8 || sq % 8 || (k_pool && (sk_b % 8 || sk_s % 8)) || (v_pool && (sv_b % 8 || sv_s % 8)))
+    return IFX_ERR_ALIGN;
+  // grid.y = parts as in the reference launch (wan.py:97): part 1 is always K
+  WanArgs a{raw,    ldraw, row,  col,   bias,   q_norm, k_norm, eps,   inv_freq, pos, ldpos, sections, q_out, sq,
+            k_pool, sk_b,  sk_s, v_pool, sv_b,  sv_s,   slots,  tokens, D,       head_dim, k_pool != nullptr,
+            v_pool != nullptr, raw_dtype == IFX_DTYPE_F32 ? 1 : 0, out_dtype};
+  if (rows > 0x7FFFFFFFLL) return IFX_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(parts));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t groups = (D / 8 + 255) / 256;
+  if (groups <= 1) hipLaunchKernelGGL(wan_qkv_kernel<1>, grid, dim3(256), 0, st, a);
+  else if (groups <= 2) hipLaunchKernelGGL(wan_qkv_kernel<2>, grid, dim3(256), 0, st, a);
+  else if (groups <= 4) hipLaunchKernelGGL(wan_qkv_kernel<4>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(wan_qkv_kernel<8>, grid, dim3(256), 0, st, a);
+  return launch_status();
+}

@@ -444,5 +444,42 @@ class QkvSplit:
                          sections=self.sec, kv_base=self.T // 2)
 
 
+class WanQkv:
+    """``wan_qkv`` after the C5 qkv projection (Wan 5B: 24 heads of 128, bias,
+    full-width q/k RMSNorm, 3-section interleaved rotary), Q dense, K/V into
+    slot rows of the pools. Algorithmic bytes: the bf16 accumulator read once,
+    Q/K/V written once (bf16), vectors once."""
+
+    def __init__(self, dev, rows=8192, H=24, HD=128, seed=0):
+        from .kernels import rope as R, wan as W
+        self.W, self.rows, self.H, self.HD = W, rows, H, HD
+        g = _gen(seed)
+        D = H * HD
+        self.raw = torch.randn(rows, 3 * D, generator=g).to(torch.bfloat16).to(dev)
+        self.row = (torch.rand(rows, generator=g) + 0.5).to(dev)
+        self.col = (torch.rand(3 * D, generator=g) + 0.5).to(dev)
+        self.bias = torch.randn(3 * D, generator=g).to(dev)
+        self.qn = (torch.rand(D, generator=g) + 0.5).to(dev)
+        self.kn = (torch.rand(D, generator=g) + 0.5).to(dev)
+        self.inv = R.rope_inv_freq(HD, 1e4, dev)
+        self.pos = torch.randint(0, 64, (rows, 3), generator=g).float().to(dev)
+        self.sec = (torch.arange(HD // 2) % 3).int().to(dev)
+        self.slots = torch.arange(rows, dtype=torch.int32, device=dev)
+        self.q = torch.empty(rows, D, dtype=torch.bfloat16, device=dev)
+        self.kp = torch.empty(1, rows, D, dtype=torch.bfloat16, device=dev)
+        self.vp = torch.empty_like(self.kp)
+        self.title = f"wan_qkv {rows} rows, {H} heads x {HD} (rescale, bias, q/k RMSNorm, 3D RoPE, KV pools)"
+
+    @property
+    def bytes(self) -> int:
+        D = self.H * self.HD
+        return 3 * self.rows * D * 2 * 2 + 3 * D * 8 + 2 * D * 4 + self.rows * (4 + 12 + 4) + self.HD * 4
+
+    def step(self, i=0):
+        self.W.wan_qkv(self.raw, self.q, heads=self.H, head_dim=self.HD, tokens=self.rows, k_pool=self.kp,
+                       v_pool=self.vp, slots=self.slots, row=self.row, col=self.col, bias=self.bias, q_norm=self.qn,
+                       k_norm=self.kn, pos=self.pos, sections=self.sec, inv_freq=self.inv)
+
+
 PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}
-CONSUMERS = {"C4": QkvSplit}
+CONSUMERS = {"C4": QkvSplit, "C5": WanQkv}

@@ -29,6 +29,11 @@ Parts
     expectation (tests/test_gi_kernels.py:58-90) evaluated with torch, by the
     rotation invariants (pair norms preserved, position 0 = identity, angle
     additivity) and by unit RMS of normalized heads.
+  * wan_qkv: the Wan QKV consumer of kernels/wan.py:19-81 (full-width q/k
+    RMSNorm, interleaved-pair rotary). Pinned against qkv_split under the
+    channel permutation that turns interleaved pairs into split halves, against
+    torch.nn.functional.rms_norm over the full width, and by the rotation
+    invariants.
 """
 from __future__ import annotations
 
@@ -297,3 +302,43 @@ def qkv_split(qkv, HQ, HKV, HD, row=None, col=None, bias=None, inv_freq=None, po
         qk = np.concatenate([lo * c - hi * s, hi * c + lo * s], axis=2)
     v = x[:, HQ + HKV:]
     return qk[:, :HQ], qk[:, HQ:], v
+
+
+def wan_qkv(raw, heads, head_dim, tokens, parts=3, row=None, col=None, bias=None, q_norm=None, k_norm=None,
+            inv_freq=None, pos=None, sections=None, eps=1e-6):
+    """Wan QKV consumer of instinctflash/kernels/wan.py:19-81, restated.
+
+    Per part p (0 = Q, 1 = K, 2 = V; columns p*D..(p+1)*D): rescale in float32 in
+    the reference's order (x*row, *col, +bias); Q and K RMS-normalized over the
+    full width D in float64 (x / sqrt(mean(x^2) + eps) * w); Q and K rotated on
+    adjacent pairs (2j, 2j+1) of every head with the float32 angle
+    pos[t, section[j]] * inv_freq[j], t = row % tokens. Returns float64 parts
+    [rows, D] in order."""
+    f32 = np.float32
+    H, HD = heads, head_dim
+    D = H * HD
+    x = np.asarray(raw, dtype=f32)[:, :parts * D]
+    rows = x.shape[0]
+    if row is not None:
+        x = (x * np.asarray(row, f32)[:, None]).astype(f32)
+    if col is not None:
+        x = (x * np.asarray(col, f32)[None, :parts * D]).astype(f32)
+    if bias is not None:
+        x = (x + np.asarray(bias, f32)[None, :parts * D]).astype(f32)
+    out = []
+    t = np.arange(rows) % tokens
+    for p in range(parts):
+        xp = x[:, p * D:(p + 1) * D].astype(np.float64)
+        w = (q_norm if p == 0 else k_norm) if p < 2 else None
+        if w is not None:
+            xp = xp / np.sqrt((xp * xp).mean(axis=1, keepdims=True) + float(f32(eps))) * np.asarray(w, np.float64)
+        if inv_freq is not None and p < 2:
+            half = HD // 2
+            sec = np.zeros(half, np.int64) if sections is None else np.asarray(sections, np.int64)
+            ang = (np.asarray(pos, f32)[t][:, sec] * np.asarray(inv_freq, f32)[None, :]).astype(f32).astype(np.float64)
+            c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+            y = xp.reshape(rows, H, half, 2)
+            e, o = y[..., 0], y[..., 1]
+            xp = np.stack([e * c - o * s, e * s + o * c], axis=-1).reshape(rows, D)
+        out.append(xp)
+    return out

@@ -416,3 +416,48 @@ def test_qkv_split_invariants(oracle_mod):
     # normalized heads have unit RMS (unit weights)
     qn, kn, _ = oracle_mod.qkv_split(raw, HQ, HKV, HD, q_norm=np.ones(HD), k_norm=np.ones(HD), eps=0.0)
     assert np.allclose(np.sqrt((qn ** 2).mean(-1)), 1.0) and np.allclose(np.sqrt((kn ** 2).mean(-1)), 1.0)
+
+
+# ---------------------------------------------------------------------------
+# wan_qkv (kernels/wan.py:19-81)
+# ---------------------------------------------------------------------------
+
+def test_wan_qkv_against_qkv_split_and_rms_norm(oracle_mod):
+    from instinctflash_amd.kernels.rope import rope_inv_freq
+    H, HD, T, B = 3, 16, 4, 2
+    D, half = H * HD, HD // 2
+    rng = np.random.default_rng(5)
+    raw = rng.standard_normal((B * T, 3 * D)).astype(np.float32)
+    inv = rope_inv_freq(HD, 1e4, "cpu").numpy()
+    pos = rng.integers(0, 50, (T, 3)).astype(np.float32)
+    sec = (np.arange(half) % 3).astype(np.int32)
+    q, k, v = oracle_mod.wan_qkv(raw, H, HD, T, inv_freq=inv, pos=pos, sections=sec)
+    # interleaved pairs (2j, 2j+1) == split halves (j, j + HD/2) after a per-head permutation
+    perm = np.concatenate([np.arange(0, HD, 2), np.arange(1, HD, 2)])
+    cols = np.concatenate([h * HD + perm for h in range(H)])
+    raw_split = np.concatenate([raw[:, p * D:(p + 1) * D][:, cols] for p in range(3)], axis=1)
+    pos_rows = pos[np.arange(B * T) % T]
+    qs, ks, vs = oracle_mod.qkv_split(raw_split, H, H, HD, inv_freq=inv, pos=pos_rows, sections=sec)
+    assert np.abs(q[:, cols] - qs.reshape(B * T, D)).max() < 1e-12
+    assert np.abs(k[:, cols] - ks.reshape(B * T, D)).max() < 1e-12
+    assert np.array_equal(v, raw[:, 2 * D:].astype(np.float64))
+    # full-width RMS norm == torch rms_norm over D
+    w = rng.random(D) + 0.5
+    qn, _ = oracle_mod.wan_qkv(raw, H, HD, T, parts=2, q_norm=w, k_norm=w)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(raw[:, :D]).double(), (D,), torch.from_numpy(w),
+                                       eps=float(np.float32(1e-6)))
+    assert np.abs(qn - ref.numpy()).max() < 1e-12
+
+
+def test_wan_qkv_rotation_invariants(oracle_mod):
+    from instinctflash_amd.kernels.rope import rope_inv_freq
+    H, HD, T = 2, 32, 3
+    D = H * HD
+    rng = np.random.default_rng(6)
+    raw = rng.standard_normal((T, 2 * D)).astype(np.float32)
+    inv = rope_inv_freq(HD, 1e4, "cpu").numpy()
+    pos = np.array([[0.0], [5.0], [900.0]], np.float32)
+    q0, _ = oracle_mod.wan_qkv(raw, H, HD, T, parts=2)
+    q, _ = oracle_mod.wan_qkv(raw, H, HD, T, parts=2, inv_freq=inv, pos=pos)
+    pair = lambda a: (a.reshape(T, -1, 2) ** 2).sum(-1)  # noqa: E731
+    assert np.allclose(pair(q), pair(q0)) and np.array_equal(q[0], q0[0])
