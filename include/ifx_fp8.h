@@ -138,6 +138,19 @@ int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, cons
                         const float* col, int act, void* q, int64_t ldq, float* scale, void* stream);
 
 /*
+ * Routed SwiGLU of a concatenated-experts gate|up accumulator gu [M, 2F] (bf16):
+ *   h[m,k] = silu(g * row[m] * col[k]) * (u * row[m] * col[F+k]) * wr
+ *   wr = route_w[m, min(k / group, E-1)] for k < n_routed, 1 for k >= n_routed
+ *   (the shared expert's columns); q, scale = per-row E4M3 of h (recipe of
+ *   ifx_quant_rows). row [M] / col [2F] f32 or NULL; route_w f32 [M, E].
+ * Replaces: instinctflash/kernels/activation.py:131-137 `moe_act_quant`
+ * (kernel :103-128), with this package's quantization recipe.
+ */
+int ifx_moe_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row, const float* col,
+                      const float* route_w, int64_t E, int64_t group, int64_t n_routed, void* q, int64_t ldq,
+                      float* scale, void* stream);
+
+/*
  * y[m,d] = x[m,d] * row[m] * col[d] + bias[d], x bf16, y bf16 or f32 (y_dtype).
  * Replaces: instinctflash/kernels/norm.py:178-185 `dequant_rows`.
  */
@@ -197,14 +210,29 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
  * Replaces: instinctflash/kernels/norm.py:97-123 `residual_norm_quant` (kernel
  * :25-94), with this package's quantization recipe (1e-12 floor, reciprocal
  * scale, IEEE division) instead of the Triton 1e-8 floor / 448/amax multiply.
- * The MoE router option (norm.py:84-94) is not provided.
+ * MoE router option (norm.py:84-94): with router_w != NULL the routing weights
+ * of ifx_moe_router are computed from the FP32 y row (before any bf16 store)
+ * and written to route_w [M, router_E]; router_bias [router_E] f32,
+ * router_E <= 256. Equal to ifx_moe_router on an F32 y, bit for bit.
  */
 int ifx_residual_norm_quant(void* res, int res_dtype, int64_t ldres, const void* delta, int delta_dtype,
                             int64_t lddelta, const float* delta_row, const float* delta_col, const float* bias,
                             const float* gate, const float* weight, const float* beta, const float* mod_scale,
                             const float* mod_shift, const int32_t* mod_index, int flags, float eps, void* q,
-                            int64_t ldq, float* q_scale, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t D,
-                            void* stream);
+                            int64_t ldq, float* q_scale, void* y, int y_dtype, int64_t ldy, const float* router_w,
+                            const float* router_bias, float* route_w, int64_t router_E, int router_top_k,
+                            float router_scale, int64_t M, int64_t D, void* stream);
+
+/*
+ * Sigmoid top-k MoE router over x [M, D] (BF16 or F32, row stride ldx):
+ *   logits = x . gate_w^T (gate_w f32 [E, D]); s = 1 / (1 + exp(-logits))
+ *   the top_k experts by s + e_bias (e_bias f32 [E]; equal values: lowest
+ *   expert index first) get route_w[m, e] = s[e] / (sum of chosen s + 1e-20) * scale,
+ *   every other expert 0.  route_w f32 [M, E].  D <= 16384, E <= 256.
+ * Replaces: instinctflash/kernels/activation.py:91-100 `moe_router` (kernel :71-88).
+ */
+int ifx_moe_router(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t D, const float* gate_w,
+                   const float* e_bias, float* route_w, int64_t E, int top_k, float scale, void* stream);
 
 /*
  * Split a fused QKV accumulator qkv [T, (HQ + 2*HKV) * HD] (BF16 or F32, row

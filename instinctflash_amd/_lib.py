@@ -75,7 +75,10 @@ SIGNATURES = {
     "ifx_quant_rows_tiled": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P]),
     "ifx_fp8_pack_skinny": (_INT, [_P, _I64, _I64, _I64, _P, _P]),
     "ifx_residual_norm_quant": (_INT, [_P, _INT, _I64, _P, _INT, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _INT,
-                                       ctypes.c_float, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _P]),
+                                       ctypes.c_float, _P, _I64, _P, _P, _INT, _I64, _P, _P, _P, _I64, _INT,
+                                       ctypes.c_float, _I64, _I64, _P]),
+    "ifx_moe_router": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _I64, _INT, ctypes.c_float, _P]),
+    "ifx_moe_act_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "ifx_quant_linear": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64, _I64,
                                 _P, _P, _SZ, _P]),
     "ifx_fp8_linear": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64,

@@ -89,14 +89,42 @@ __device__ __forceinline__ float clamp_fp8(float v) {
   return v != v ? v : fminf(fmaxf(v, -kFp8Max), kFp8Max);
 }
 
-// Wave-wide (64 lanes) max of an unsigned value.
+// Wave-wide (64 lanes) reductions through DPP lane moves within each 16-lane
+// row (quad swaps, then the half-row and row mirrors), then the four row
+// results read as scalars: no LDS round trips, and every lane returns the same
+// value in a fixed combination order. All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF,
+                                                           0xF, false));
+}
+
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppRowMirror = 0x140;  // row_mirror
+
+__device__ __forceinline__ uint32_t row_lane(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    uint32_t o = __shfl_xor(v, off, 64);
-    v = v > o ? v : o;
-  }
-  return v;
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, dpp_u32<kDppQuadSwap1>(v));
+  v = mx(v, dpp_u32<kDppQuadSwap2>(v));
+  v = mx(v, dpp_u32<kDppHalfMirror>(v));
+  v = mx(v, dpp_u32<kDppRowMirror>(v));
+  return mx(mx(row_lane(v, 0), row_lane(v, 16)), mx(row_lane(v, 32), row_lane(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v = v + __uint_as_float(dpp_u32<kDppQuadSwap1>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<kDppQuadSwap2>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(v)));
+  const uint32_t b = __float_as_uint(v);
+  return (__uint_as_float(row_lane(b, 0)) + __uint_as_float(row_lane(b, 16))) +
+         (__uint_as_float(row_lane(b, 32)) + __uint_as_float(row_lane(b, 48)));
 }
 
 // GELU, tanh form: 0.5*x*(1+tanh(u)), u = sqrt(2/pi)*(x + 0.044715 x^3).

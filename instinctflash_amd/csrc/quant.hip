@@ -34,13 +34,27 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// ---- row sources: produce 8 consecutive FP32 values of row m --------------
+// ---- row sources -----------------------------------------------------------
+// Each source produces FP32 values of row m in two forms:
+//  * fetch(m, k, raw) issues every load of the 8 elements k..k+7 with no
+//    branch (m and k must be in range), finish(raw, m, k, v) turns them into
+//    values: the register-resident kernel issues the fetches of all its groups
+//    before the first finish, so a row's loads are in flight together instead
+//    of one memory latency per group;
+//  * load1(m, k): one element, for the two-pass kernel.
+// Optional column vectors are template flags so that fetch stays branch-free;
+// the per-row scale is read once per row by begin(m).
 
 struct SrcBf16 {
   const uint16_t* x;
   int64_t ldx;
-  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
-    unpack_bf16x8(*reinterpret_cast<const uint4*>(x + m * ldx + k), v);
+  struct Raw { uint4 a; };
+  __device__ __forceinline__ float begin(int64_t) const { return 1.0f; }
+  __device__ __forceinline__ void fetch(int64_t m, int64_t k, Raw& r) const {
+    r.a = *reinterpret_cast<const uint4*>(x + m * ldx + k);
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float, int64_t, int64_t, float* v) const {
+    unpack_bf16x8(r.a, v);
   }
   __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
     return bf16_bits_to_f32(x[m * ldx + k]);
@@ -50,16 +64,34 @@ struct SrcBf16 {
 struct SrcF32 {
   const float* x;
   int64_t ldx;
-  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
-    const float4 a = *reinterpret_cast<const float4*>(x + m * ldx + k);
-    const float4 b = *reinterpret_cast<const float4*>(x + m * ldx + k + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  struct Raw { float4 a, b; };
+  __device__ __forceinline__ float begin(int64_t) const { return 1.0f; }
+  __device__ __forceinline__ void fetch(int64_t m, int64_t k, Raw& r) const {
+    r.a = *reinterpret_cast<const float4*>(x + m * ldx + k);
+    r.b = *reinterpret_cast<const float4*>(x + m * ldx + k + 4);
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float, int64_t, int64_t, float* v) const {
+    v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+    v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
   }
   __device__ __forceinline__ float load1(int64_t m, int64_t k) const { return x[m * ldx + k]; }
 };
 
+struct Vec8 {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ float operator[](int i) const {
+    const float t[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    return t[i];
+  }
+};
+
 // v = x*row[m]*col[k] + bias[k] (-> gelu_tanh); reference kernels/norm.py:135-144.
+// HC / HB: col / bias present (vector fetch only; load1 tests the pointers).
+template <bool HC = true, bool HB = true>
 struct SrcAffine {
   const uint16_t* x;
   int64_t ldx;
@@ -67,25 +99,32 @@ struct SrcAffine {
   const float* col;
   const float* bias;
   int gelu;
-  __device__ __forceinline__ float op(float v, int64_t m, float c, float b) const {
-    if (row) v = v * row[m];
+  struct Raw { uint4 a; Vec8 c, b; };
+  __device__ __forceinline__ float op(float v, float r, float c, float b) const {
+    if (row) v = v * r;
     if (col) v = v * c;
     if (bias) v = v + b;
     if (gelu) v = gelu_tanh(v);
     return v;
   }
-  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
-    unpack_bf16x8(*reinterpret_cast<const uint4*>(x + m * ldx + k), v);
+  __device__ __forceinline__ float begin(int64_t m) const { return row ? row[m] : 1.0f; }
+  __device__ __forceinline__ void fetch(int64_t m, int64_t k, Raw& r) const {
+    r.a = *reinterpret_cast<const uint4*>(x + m * ldx + k);
+    if constexpr (HC) r.c.load(col + k);
+    if constexpr (HB) r.b.load(bias + k);
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float rs, int64_t, int64_t, float* v) const {
+    unpack_bf16x8(r.a, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      v[i] = op(v[i], m, col ? col[k + i] : 1.0f, bias ? bias[k + i] : 0.0f);
+    for (int i = 0; i < 8; ++i) v[i] = op(v[i], rs, HC ? r.c[i] : 1.0f, HB ? r.b[i] : 0.0f);
   }
   __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
-    return op(bf16_bits_to_f32(x[m * ldx + k]), m, col ? col[k] : 1.0f, bias ? bias[k] : 0.0f);
+    return op(bf16_bits_to_f32(x[m * ldx + k]), row ? row[m] : 1.0f, col ? col[k] : 1.0f, bias ? bias[k] : 0.0f);
   }
 };
 
 // h = act(g)*u from a gate|up accumulator; reference kernels/activation.py:26-40.
+template <bool HC = true>
 struct SrcGated {
   const uint16_t* gu;
   int64_t ldgu;
@@ -93,31 +132,72 @@ struct SrcGated {
   const float* row;
   const float* col;
   int act;
-  __device__ __forceinline__ float op(float g, float u, int64_t m, int64_t k) const {
+  struct Raw { uint4 g, u; Vec8 cg, cu; };
+  __device__ __forceinline__ float op(float g, float u, float r, float cg, float cu) const {
     if (row) {
-      const float r = row[m];
       g = g * r;
       u = u * r;
     }
     if (col) {
-      g = g * col[k];
-      u = u * col[F + k];
+      g = g * cg;
+      u = u * cu;
     }
     const float a = act == IFX_ACT_SILU ? silu(g) : gelu_tanh(g);
     return a * u;
   }
-  __device__ __forceinline__ void load8(int64_t m, int64_t k, float* v) const {
+  __device__ __forceinline__ float begin(int64_t m) const { return row ? row[m] : 1.0f; }
+  __device__ __forceinline__ void fetch(int64_t m, int64_t k, Raw& r) const {
+    r.g = *reinterpret_cast<const uint4*>(gu + m * ldgu + k);
+    r.u = *reinterpret_cast<const uint4*>(gu + m * ldgu + F + k);
+    if constexpr (HC) {
+      r.cg.load(col + k);
+      r.cu.load(col + F + k);
+    }
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float rs, int64_t, int64_t, float* v) const {
     float g[8], u[8];
-    unpack_bf16x8(*reinterpret_cast<const uint4*>(gu + m * ldgu + k), g);
-    unpack_bf16x8(*reinterpret_cast<const uint4*>(gu + m * ldgu + F + k), u);
+    unpack_bf16x8(r.g, g);
+    unpack_bf16x8(r.u, u);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = op(g[i], u[i], m, k + i);
+    for (int i = 0; i < 8; ++i) v[i] = op(g[i], u[i], rs, HC ? r.cg[i] : 1.0f, HC ? r.cu[i] : 1.0f);
   }
   __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
-    return op(bf16_bits_to_f32(gu[m * ldgu + k]), bf16_bits_to_f32(gu[m * ldgu + F + k]), m, k);
+    return op(bf16_bits_to_f32(gu[m * ldgu + k]), bf16_bits_to_f32(gu[m * ldgu + F + k]), row ? row[m] : 1.0f,
+              col ? col[k] : 1.0f, col ? col[F + k] : 1.0f);
   }
 };
 
+// h = silu(g)*u*wr with the routing weight wr = route_w[m, min(k/group, E-1)] for
+// routed columns k < n_routed and 1 for the shared expert's columns; reference
+// kernels/activation.py:103-128. The vector fetch needs group % 8 == 0 and
+// n_routed % 8 == 0 (one weight per 8-column group) and route_w != NULL.
+template <bool HC = true>
+struct SrcMoe {
+  SrcGated<HC> base;  // act is always SiLU
+  const float* rw;
+  int64_t E;
+  int64_t group;
+  int64_t n_routed;
+  struct Raw { typename SrcGated<HC>::Raw b; float w; };
+  __device__ __forceinline__ int64_t expert(int64_t k) const {
+    const int64_t e = k / group;
+    return e < E - 1 ? e : E - 1;
+  }
+  __device__ __forceinline__ float begin(int64_t m) const { return base.begin(m); }
+  __device__ __forceinline__ void fetch(int64_t m, int64_t k, Raw& r) const {
+    base.fetch(m, k, r.b);
+    r.w = rw[m * E + expert(k)];
+  }
+  __device__ __forceinline__ void finish(const Raw& r, float rs, int64_t m, int64_t k, float* v) const {
+    base.finish(r.b, rs, m, k, v);
+    const float w = k < n_routed ? r.w : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * w;
+  }
+  __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
+    return base.load1(m, k) * (k < n_routed ? rw[m * E + expert(k)] : 1.0f);
+  }
+};
 
 // Team-wide max: lanes [team*T, team*T+T) of the block.
 template <int T>
@@ -148,25 +228,40 @@ __device__ __forceinline__ int64_t tile_offset(int64_t m, int64_t k, int64_t ks)
 // ks == 0: q is row-major with stride ldq. ks > 0: q is the skinny tile layout
 // (rows M..16*ceil(M/16)-1 and K bytes K..128*ks-1 are written as zeros, by the
 // launch covering m_rows = 16*ceil(M/16) rows).
-template <int T, int VPT, class Src>
-__global__ __launch_bounds__(kBlock) void quant_rows_vec(Src src, int64_t M, int64_t K, uint8_t* q,
-                                                        int64_t ldq, float* scale, int64_t ks, int64_t m_rows) {
-  __shared__ uint32_t red[kBlock / 64];
-  constexpr int R = kBlock / T;
+// BLK lanes per workgroup: R = BLK / T rows per workgroup.
+template <int T, int VPT, class Src, int BLK = kBlock>
+__global__ __launch_bounds__(BLK) void quant_rows_vec(Src src, int64_t M, int64_t K, uint8_t* q,
+                                                     int64_t ldq, float* scale, int64_t ks, int64_t m_rows) {
+  __shared__ uint32_t red[BLK / 64];
+  constexpr int R = BLK / T;
   const int lt = threadIdx.x % T;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * R + threadIdx.x / T;
   const bool row_ok = m < M;
   const int64_t nvec = K >> 3;
+  // the loads of up to 8 groups first (clamped into range, so no branch), then
+  // their math: one memory latency per batch of 8 groups
+  constexpr int kMaxBatch = BLK >= 1024 ? 2 : 8;  // 128 VGPRs per lane at 1024 lanes
+  constexpr int kBatch = VPT < kMaxBatch ? VPT : kMaxBatch;
+  const int64_t mc = row_ok ? m : M - 1;
+  const float rs = src.begin(mc);
   float v[VPT][8];
   uint32_t amax = 0;
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int64_t idx = lt + static_cast<int64_t>(j) * T;
-    if (row_ok && idx < nvec) {
-      src.load8(m, idx * 8, v[j]);
+  for (int j0 = 0; j0 < VPT; j0 += kBatch) {
+    typename Src::Raw raw[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t idx = lt + static_cast<int64_t>(j0 + j) * T;
+      src.fetch(mc, (idx < nvec ? idx : nvec - 1) * 8, raw[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t idx = lt + static_cast<int64_t>(j0 + j) * T;
+      src.finish(raw[j], rs, mc, (idx < nvec ? idx : nvec - 1) * 8, v[j0 + j]);
+      const bool on = row_ok && idx < nvec;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const uint32_t b = abs_bits(v[j][i]);
+        const uint32_t b = on ? abs_bits(v[j0 + j][i]) : 0u;
         amax = amax > b ? amax : b;
       }
     }
@@ -216,13 +311,13 @@ __global__ __launch_bounds__(kBlock) void quant_rows_generic(Src src, int64_t M,
     q[m * ldq + k] = static_cast<uint8_t>(q1(src.load1(m, k), s));
 }
 
-template <int T, int VPT, class Src>
+template <int T, int VPT, class Src, int BLK = kBlock>
 void launch_vec(const Src& src, int64_t M, int64_t K, uint8_t* q, int64_t ldq, float* scale,
                 hipStream_t st, int64_t ks = 0) {
-  constexpr int R = kBlock / T;
+  constexpr int R = BLK / T;
   const int64_t m_rows = ks > 0 ? (M + 15) / 16 * 16 : M;
   const int64_t grid = (m_rows + R - 1) / R;
-  hipLaunchKernelGGL((quant_rows_vec<T, VPT, Src>), dim3(static_cast<unsigned>(grid)), dim3(kBlock),
+  hipLaunchKernelGGL((quant_rows_vec<T, VPT, Src, BLK>), dim3(static_cast<unsigned>(grid)), dim3(BLK),
                      0, st, src, M, K, q, ldq, scale, ks, m_rows);
 }
 
@@ -237,13 +332,15 @@ int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q,
   }
   if (M > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
   const int64_t nvec = K / 8;
-  if (vec_ok && K % 8 == 0 && nvec <= 2048 && M < 256) {
-    // Few rows: latency-bound, so give every row a whole 256-lane block (one
-    // or two loads per lane in flight) instead of packing rows per block.
+  if (vec_ok && K % 8 == 0 && nvec <= 4096 && M < 256) {
+    // Few rows: latency-bound, so give every row a whole 256-lane block
+    // instead of packing rows per block; wide rows get up to 1024 lanes, so
+    // that each SIMD interleaves several waves of the row's arithmetic.
     if (nvec <= 256) launch_vec<256, 1>(src, M, K, q, ldq, scale, st);
-    else if (nvec <= 512) launch_vec<256, 2>(src, M, K, q, ldq, scale, st);
-    else if (nvec <= 1024) launch_vec<256, 4>(src, M, K, q, ldq, scale, st);
-    else launch_vec<256, 8>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 512) launch_vec<512, 1, Src, 512>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 1024) launch_vec<1024, 1, Src, 1024>(src, M, K, q, ldq, scale, st);
+    else if (nvec <= 2048) launch_vec<1024, 2, Src, 1024>(src, M, K, q, ldq, scale, st);
+    else launch_vec<1024, 4, Src, 1024>(src, M, K, q, ldq, scale, st);
   } else if (vec_ok && K % 8 == 0 && nvec <= 2048) {
     if (nvec <= 64) launch_vec<64, 1>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 128) launch_vec<64, 2>(src, M, K, q, ldq, scale, st);
@@ -251,6 +348,8 @@ int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q,
     else if (nvec <= 512) launch_vec<64, 8>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 1024) launch_vec<128, 8>(src, M, K, q, ldq, scale, st);
     else launch_vec<256, 8>(src, M, K, q, ldq, scale, st);
+  } else if (vec_ok && K % 8 == 0 && nvec <= 4096) {
+    launch_vec<256, 16>(src, M, K, q, ldq, scale, st);
   } else {
     hipLaunchKernelGGL((quant_rows_generic<Src>), dim3(static_cast<unsigned>(M)), dim3(kBlock), 0, st,
                        src, M, K, q, ldq, scale);
@@ -426,9 +525,9 @@ int ifx_quant_rows_tiled(const void* x, int x_dtype, int64_t ldx, int64_t M, int
   auto go = [&](const auto& src) {
     using S = std::decay_t<decltype(src)>;
     if (nvec <= 256) launch_vec<256, 1, S>(src, M, K, qb, 0, scale, st, ks);
-    else if (nvec <= 512) launch_vec<256, 2, S>(src, M, K, qb, 0, scale, st, ks);
-    else if (nvec <= 1024) launch_vec<256, 4, S>(src, M, K, qb, 0, scale, st, ks);
-    else launch_vec<256, 8, S>(src, M, K, qb, 0, scale, st, ks);
+    else if (nvec <= 512) launch_vec<512, 1, S, 512>(src, M, K, qb, 0, scale, st, ks);
+    else if (nvec <= 1024) launch_vec<1024, 1, S, 1024>(src, M, K, qb, 0, scale, st, ks);
+    else launch_vec<1024, 2, S, 1024>(src, M, K, qb, 0, scale, st, ks);
   };
   if (f32) go(SrcF32{static_cast<const float*>(x), ldx});
   else go(SrcBf16{static_cast<const uint16_t*>(x), ldx});
@@ -501,11 +600,19 @@ int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float*
                   float* scale, void* stream) {
   if (M < 0 || K < 0 || ldx < K || ldq < K) return IFX_ERR_INVALID;
   if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
-  SrcAffine s{static_cast<const uint16_t*>(x), ldx, row, col, bias, gelu ? 1 : 0};
-  const bool vec_ok = aligned16(x) && ldx % 8 == 0 &&
-                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
-  return dispatch_rows(s, vec_ok, M, K, static_cast<uint8_t*>(q), ldq, scale,
-                       static_cast<hipStream_t>(stream));
+  const bool vec_ok = aligned16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 &&
+                      aligned16(col) && aligned16(bias);
+  auto go = [&](auto s) {
+    s.x = static_cast<const uint16_t*>(x);
+    s.ldx = ldx;
+    s.row = row;
+    s.col = col;
+    s.bias = bias;
+    s.gelu = gelu ? 1 : 0;
+    return dispatch_rows(s, vec_ok, M, K, static_cast<uint8_t*>(q), ldq, scale, static_cast<hipStream_t>(stream));
+  };
+  if (col) return bias ? go(SrcAffine<true, true>{}) : go(SrcAffine<true, false>{});
+  return bias ? go(SrcAffine<false, true>{}) : go(SrcAffine<false, false>{});
 }
 
 int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row,
@@ -513,11 +620,33 @@ int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, cons
   if (M < 0 || F < 0 || ldgu < 2 * F || ldq < F) return IFX_ERR_INVALID;
   if (act != IFX_ACT_GELU_TANH && act != IFX_ACT_SILU) return IFX_ERR_INVALID;
   if (M > 0 && (!gu || !q || !scale)) return IFX_ERR_INVALID;
-  SrcGated s{static_cast<const uint16_t*>(gu), ldgu, F, row, col, act};
   const bool vec_ok = aligned16(gu) && ldgu % 8 == 0 && F % 8 == 0 &&
-                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0;
-  return dispatch_rows(s, vec_ok, M, F, static_cast<uint8_t*>(q), ldq, scale,
-                       static_cast<hipStream_t>(stream));
+                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 && aligned16(col);
+  const uint16_t* g = static_cast<const uint16_t*>(gu);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (col) return dispatch_rows(SrcGated<true>{g, ldgu, F, row, col, act}, vec_ok, M, F, static_cast<uint8_t*>(q),
+                                ldq, scale, st);
+  return dispatch_rows(SrcGated<false>{g, ldgu, F, row, col, act}, vec_ok, M, F, static_cast<uint8_t*>(q), ldq,
+                       scale, st);
+}
+
+int ifx_moe_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row, const float* col,
+                      const float* route_w, int64_t E, int64_t group, int64_t n_routed, void* q, int64_t ldq,
+                      float* scale, void* stream) {
+  if (M < 0 || F < 0 || ldgu < 2 * F || ldq < F || E <= 0 || group <= 0 || n_routed < 0) return IFX_ERR_INVALID;
+  if (M > 0 && (!gu || !q || !scale || (n_routed > 0 && !route_w))) return IFX_ERR_INVALID;
+  if (n_routed == 0)  // no routed columns: the plain SwiGLU
+    return ifx_gated_act_quant(gu, ldgu, M, F, row, col, IFX_ACT_SILU, q, ldq, scale, stream);
+  const bool vec_ok = aligned16(gu) && ldgu % 8 == 0 && F % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 && aligned16(col) &&
+                      group % 8 == 0 && n_routed % 8 == 0;
+  const uint16_t* g = static_cast<const uint16_t*>(gu);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (col)
+    return dispatch_rows(SrcMoe<true>{{g, ldgu, F, row, col, IFX_ACT_SILU}, route_w, E, group, n_routed}, vec_ok, M,
+                         F, static_cast<uint8_t*>(q), ldq, scale, st);
+  return dispatch_rows(SrcMoe<false>{{g, ldgu, F, row, col, IFX_ACT_SILU}, route_w, E, group, n_routed}, vec_ok, M,
+                       F, static_cast<uint8_t*>(q), ldq, scale, st);
 }
 
 int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const float* row,

@@ -159,8 +159,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_split_kernel(QkvArgs 
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) ss = ss + (lo[j] * lo[j] + hi[j] * hi[j]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
+        ss = wave_sum_f32(ss);
         const float rs = 1.0f / __builtin_sqrtf(ss / static_cast<float>(a.HD) + a.eps);
         const float* w = h < a.HQ ? a.qnw : a.knw;
 #pragma unroll
@@ -285,8 +284,7 @@ __global__ __launch_bounds__(256) void wan_qkv_kernel(WanArgs a) {
     for (int e = 0; e < 8; ++e) ss = ss + x[jv][e] * x[jv][e];
   }
   if (nw) {  // block-uniform
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
+    ss = wave_sum_f32(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float tot = red[0] + red[1] + red[2] + red[3];

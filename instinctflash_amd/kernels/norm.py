@@ -79,9 +79,10 @@ def residual_norm_quant(res, *, delta=None, delta_row=None, delta_col=None, bias
     the int32 ``mod_index``). The quantization is this package's recipe
     (1e-12 floor, scale = amax * fl32(1/448), IEEE division) rather than the
     Triton kernel's 1e-8 floor and 448/amax multiply. ``num_warps`` is accepted
-    for signature compatibility. The MoE ``router`` option is not provided."""
-    if router is not None:
-        raise ValueError("residual_norm_quant: the MoE router option is not provided by the gfx950 FP8 path")
+    for signature compatibility. ``router=(gate_w [E, D], e_bias [E], out [M, E],
+    top_k, scale)`` also writes the MoE routing weights of ``moe_router``
+    computed from the float32 normalized row (norm.py:84-94), equal bit for bit
+    to ``moe_router`` on a float32 ``y``."""
     if res.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("res must be float32 or bfloat16")
     M, D, ldres = _rows("res", res, res.dtype)
@@ -116,9 +117,23 @@ def residual_norm_quant(res, *, delta=None, delta_row=None, delta_col=None, bias
         My, _, ldy = _rows("y", y, y.dtype, dev, cols=D)
         if My != M:
             raise ValueError("y must have as many rows as res")
+    rw = rb = ro = None
+    rE, rK, rS = 0, 0, 1.0
+    if router is not None:
+        from .activation import _f32_matrix
+        if len(router) != 5:
+            raise ValueError("router must be (gate_w, e_bias, out, top_k, scale)")
+        rw, rb, ro, rK, rS = router
+        rE = rw.shape[0] if rw.dim() == 2 else -1
+        _f32_matrix("router gate_w", rw, rE, D, dev)
+        _vec("router e_bias", rb, rE, device=dev)
+        _f32_matrix("router out", ro, M, rE, dev)
+        if not 0 <= int(rK) <= rE:
+            raise ValueError(f"router top_k must be in [0, {rE}]")
     dt = lambda t: _lib.DTYPE_F32 if t is not None and t.dtype == torch.float32 else _lib.DTYPE_BF16  # noqa: E731
     flags = (_lib.RNQ_WRITE_RES if write_res else 0) | (_lib.RNQ_LAYERNORM if layernorm else 0)
     _lib.check(_lib.load().ifx_residual_norm_quant(
         _ptr(res), dt(res), ldres, _ptr(delta), dt(delta), lddelta, _ptr(delta_row), _ptr(delta_col), _ptr(bias),
         _ptr(gate), _ptr(weight), _ptr(beta), _ptr(mod_scale), _ptr(mod_shift), _ptr(mod_index), flags, float(eps),
-        _ptr(q), ldq, _ptr(q_scale), _ptr(y), dt(y), ldy, M, D, _stream(dev)), "ifx_residual_norm_quant")
+        _ptr(q), ldq, _ptr(q_scale), _ptr(y), dt(y), ldy, _ptr(rw), _ptr(rb), _ptr(ro), rE, int(rK), float(rS), M, D,
+        _stream(dev)), "ifx_residual_norm_quant")

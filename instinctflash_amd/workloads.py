@@ -481,5 +481,62 @@ class WanQkv:
                        k_norm=self.kn, pos=self.pos, sections=self.sec, inv_freq=self.inv)
 
 
+class MoeRoute:
+    """The MoE layer's pre-norm with the fused router (``residual_norm_quant``
+    with ``router=``) at the vla2 action-expert shape: 51 suffix tokens x 768,
+    32 experts, top 4. Algorithmic bytes: res read + write (8 B), bf16 delta
+    (2 B), q (1 B) per element, the fp32 router matrix [E, D] once, the routing
+    weights [M, E] written, vectors once."""
+
+    def __init__(self, dev, M=51, D=768, E=32, seed=0):
+        from .kernels import norm as N
+        self.N, self.M, self.D, self.E = N, M, D, E
+        g = _gen(seed)
+        f = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+        self.t = dict(res=f(M, D), delta=f(M, D).to(torch.bfloat16), delta_row=f(M).abs(), delta_col=f(D).abs(),
+                      mod_scale=f(D) * 0.1, mod_shift=f(D) * 0.1)
+        self.router = (f(E, D) * 0.05, f(E).abs() * 0.01, torch.empty(M, E, device=dev), 4, 4.0)
+        self.q = torch.empty((M, D), dtype=F.E4M3, device=dev)
+        self.qs = torch.empty(M, dtype=torch.float32, device=dev)
+        self.title = f"residual_norm_quant + router {M}x{D}, {E} experts top 4 (vla2 MoE pre-norm)"
+
+    @property
+    def bytes(self) -> int:
+        return 11 * self.M * self.D + 3 * 4 * self.D + 2 * 4 * self.M + 4 * self.E * self.D + 4 * self.E * (self.M + 1)
+
+    def step(self, i=0):
+        self.N.residual_norm_quant(self.t["res"], delta=self.t["delta"], delta_row=self.t["delta_row"],
+                                   delta_col=self.t["delta_col"], mod_scale=self.t["mod_scale"],
+                                   mod_shift=self.t["mod_shift"], q=self.q, q_scale=self.qs, router=self.router)
+
+
+class MoeAct:
+    """``moe_act_quant`` at the vla2 MoE shape: 51 tokens, 32 routed experts x 512
+    + 704 shared columns (F = 17088). Algorithmic bytes: the bf16 gate|up
+    accumulator read (4 B per output column), q written (1 B), col [2F] and the
+    routing weights once, row and q_scale per row."""
+
+    def __init__(self, dev, M=51, E=32, G=512, S=704, seed=0):
+        from .kernels import activation as A
+        self.A, self.M, self.E, self.G = A, M, E, G
+        self.F = F_ = E * G + S
+        g = _gen(seed)
+        self.gu = torch.randn(M, 2 * F_, generator=g).to(torch.bfloat16).to(dev)
+        self.row = (torch.rand(M, generator=g) + 0.5).to(dev)
+        self.col = (torch.rand(2 * F_, generator=g) + 0.5).to(dev)
+        self.rw = torch.rand(M, E, generator=g).to(dev)
+        self.q = torch.empty((M, F_), dtype=F.E4M3, device=dev)
+        self.qs = torch.empty(M, dtype=torch.float32, device=dev)
+        self.title = f"moe_act_quant {M}x{F_} ({E} experts x {G} + {S} shared, routed SwiGLU, e4m3)"
+
+    @property
+    def bytes(self) -> int:
+        return 5 * self.M * self.F + 8 * self.F + 4 * self.M * (self.E + 2)
+
+    def step(self, i=0):
+        self.A.moe_act_quant(self.gu, self.q, self.qs, self.rw, row=self.row, col=self.col, experts=self.E,
+                             group=self.G, n_routed=self.E * self.G)
+
+
 PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}
-CONSUMERS = {"C4": QkvSplit, "C5": WanQkv}
+CONSUMERS = {"C4": QkvSplit, "C5": WanQkv, "vla2 MoE": MoeRoute, "vla2 MoE act": MoeAct}

@@ -34,6 +34,15 @@ Parts
     channel permutation that turns interleaved pairs into split halves, against
     torch.nn.functional.rms_norm over the full width, and by the rotation
     invariants.
+  * moe_router / moe_act: the MoE routing of kernels/activation.py:71-137
+    (sigmoid top-k router, routed SwiGLU with per-expert column weights).
+    moe_router is pinned by the reference test's own construction
+    (tests/test_gi_kernels.py:179-192: torch.topk + scatter + renormalize), by
+    a brute-force search over every top_k-subset of experts and by the
+    invariants (weights sum to scale, E - top_k zeros, bias moves selection but
+    not weights); moe_act by the reference test's repeat_interleave
+    construction of the column weights (:193-203), by reduction to the plain
+    SwiGLU with unit weights, and by linearity in the routing weight.
 """
 from __future__ import annotations
 
@@ -342,3 +351,41 @@ def wan_qkv(raw, heads, head_dim, tokens, parts=3, row=None, col=None, bias=None
             xp = np.stack([e * c - o * s, e * s + o * c], axis=-1).reshape(rows, D)
         out.append(xp)
     return out
+
+
+def moe_router(x, gate_w, e_bias, top_k, scale):
+    """Sigmoid top-k router of instinctflash/kernels/activation.py:71-88, restated.
+
+    logits = x . gate_w^T and s = sigmoid(logits) in float64; the top_k experts
+    by s + e_bias (equal scores: lowest expert index first, as the repeated
+    argmax of :82-85) get s / (sum of chosen s + 1e-20) * scale, the others 0.
+    Returns (route_w float64 [M, E], sel float64 [M, E] the selection scores)."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(gate_w, np.float64)
+    sg = 1.0 / (1.0 + np.exp(-(x @ w.T)))
+    sel = sg + np.asarray(e_bias, np.float64)[None, :]
+    M, E = sel.shape
+    out = np.zeros((M, E))
+    order = np.argsort(-sel, axis=1, kind="stable")[:, :top_k]
+    rows = np.arange(M)[:, None]
+    out[rows, order] = sg[rows, order]
+    out = out / (out.sum(axis=1, keepdims=True) + 1e-20) * scale
+    return out, sel
+
+
+def moe_act(gu, row, col, route_w, experts, group, n_routed):
+    """Routed SwiGLU of instinctflash/kernels/activation.py:103-128, restated in
+    float32 in the reference's order: g = gu_g*row*col_g, u = gu_u*row*col_u,
+    h = silu(g) * u * wr, wr = route_w[m, min(c // group, experts - 1)] for
+    c < n_routed else 1. gu: float32 [M, 2F]. Returns h float32 [M, F]."""
+    f32 = np.float32
+    gu = np.asarray(gu, f32)
+    F = gu.shape[1] // 2
+    r = np.asarray(row, f32)[:, None]
+    c = np.asarray(col, f32)[None, :]
+    g = (gu[:, :F] * r).astype(f32) * c[:, :F]
+    u = (gu[:, F:] * r).astype(f32) * c[:, F:]
+    cols = np.arange(F)
+    grp = np.minimum(cols // group, experts - 1)
+    wr = np.where(cols[None, :] < n_routed, np.asarray(route_w, f32)[:, grp], f32(1.0)).astype(f32)
+    return ((silu(g.astype(f32)) * u).astype(f32) * wr).astype(f32)

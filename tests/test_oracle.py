@@ -461,3 +461,71 @@ def test_wan_qkv_rotation_invariants(oracle_mod):
     q, _ = oracle_mod.wan_qkv(raw, H, HD, T, parts=2, inv_freq=inv, pos=pos)
     pair = lambda a: (a.reshape(T, -1, 2) ** 2).sum(-1)  # noqa: E731
     assert np.allclose(pair(q), pair(q0)) and np.array_equal(q[0], q0[0])
+
+
+def test_moe_router_matches_reference_test_construction(oracle_mod):
+    # tests/test_gi_kernels.py:179-192: topk of sigmoid + bias, scatter the
+    # unbiased sigmoid, renormalize to `scale`.
+    g = torch.Generator().manual_seed(7)
+    M, D, E = 51, 768, 32
+    x = torch.randn(M, D, generator=g, dtype=torch.float64)
+    gw = torch.randn(E, D, generator=g, dtype=torch.float64) * 0.05
+    eb = torch.rand(E, generator=g, dtype=torch.float64) * 0.01
+    got, _ = oracle_mod.moe_router(x.numpy(), gw.numpy(), eb.numpy(), 4, 4.0)
+    s = torch.sigmoid(x @ gw.t())
+    idx = torch.topk(s + eb, 4, -1).indices
+    ref = torch.zeros(M, E, dtype=torch.float64).scatter(1, idx, s.gather(1, idx))
+    ref = ref / (ref.sum(-1, keepdim=True) + 1e-20) * 4.0
+    assert np.abs(got - ref.numpy()).max() < 1e-12
+
+
+def test_moe_router_brute_force_and_invariants(oracle_mod):
+    import itertools
+    rng = np.random.default_rng(3)
+    M, D, E, K = 20, 16, 7, 3
+    x = rng.standard_normal((M, D))
+    gw = rng.standard_normal((E, D)) * 0.3
+    eb = rng.standard_normal(E) * 0.2
+    got, sel = oracle_mod.moe_router(x, gw, eb, K, 2.5)
+    sg = 1.0 / (1.0 + np.exp(-(x @ gw.T)))
+    for m in range(M):
+        # the chosen set maximizes the summed selection score over all K-subsets
+        best = max(itertools.combinations(range(E), K), key=lambda c: sum(sel[m, list(c)]))
+        assert set(np.nonzero(got[m])[0]) == set(best)
+        w = sg[m, list(best)]
+        assert np.allclose(got[m, list(best)], w / w.sum() * 2.5, rtol=1e-14)
+    assert np.allclose(got.sum(1), 2.5) and ((got == 0).sum(1) == E - K).all()
+    # the bias moves selection only: a huge bias on expert 0 forces it in with its unbiased weight
+    eb2 = eb.copy()
+    eb2[0] = 100.0
+    got2, _ = oracle_mod.moe_router(x, gw, eb2, K, 2.5)
+    chosen_sum = np.where(got2 > 0, sg, 0.0).sum(1)
+    assert (got2[:, 0] > 0).all() and np.allclose(got2[:, 0], 2.5 * sg[:, 0] / chosen_sum, rtol=1e-14)
+    # equal scores pick the lowest index (repeated argmax)
+    tie, _ = oracle_mod.moe_router(np.zeros((1, D)), gw, np.zeros(E), K, 1.0)
+    assert np.array_equal(np.nonzero(tie[0])[0], np.arange(K)) and np.allclose(tie[0, :K], 1.0 / K)
+
+
+def test_moe_act_matches_reference_test_construction(oracle_mod):
+    # tests/test_gi_kernels.py:193-203: column weights by repeat_interleave of
+    # the routing weights over each expert's group, ones for the shared expert.
+    g = torch.Generator().manual_seed(5)
+    M, E, G, S = 6, 4, 16, 24
+    F = E * G + S
+    gu = torch.randn(M, 2 * F, generator=g)
+    row, col = torch.rand(M, generator=g) + 0.5, torch.rand(2 * F, generator=g) + 0.5
+    rw = torch.rand(M, E, generator=g)
+    h = oracle_mod.moe_act(gu.numpy(), row.numpy(), col.numpy(), rw.numpy(), E, G, E * G)
+    xg = gu.double() * row.double()[:, None] * col.double()
+    wcol = torch.cat([rw.double().repeat_interleave(G, 1), torch.ones(M, S, dtype=torch.float64)], 1)
+    ref = torch.nn.functional.silu(xg[:, :F]) * xg[:, F:] * wcol
+    assert np.abs(h - ref.numpy()).max() <= 1e-5 * np.abs(ref.numpy()).max()
+    # unit routing weights reduce it to the plain SwiGLU of gated_act_quant
+    plain = oracle_mod.moe_act(gu.numpy(), row.numpy(), col.numpy(), np.ones((M, E), np.float32), E, G, E * G)
+    sw = torch.nn.functional.silu(xg[:, :F]) * xg[:, F:]
+    assert np.abs(plain - sw.numpy()).max() <= 1e-5 * np.abs(sw.numpy()).max()
+    # n_routed beyond E*G clamps to the last expert's weight
+    cl = oracle_mod.moe_act(gu.numpy(), row.numpy(), col.numpy(), rw.numpy(), E, G, F)
+    ratio = cl[:, E * G:] / np.where(plain[:, E * G:] == 0, 1, plain[:, E * G:])
+    nz = plain[:, E * G:] != 0
+    assert np.allclose(ratio[nz], np.broadcast_to(rw.numpy()[:, E - 1:E], ratio.shape)[nz], rtol=1e-6)
