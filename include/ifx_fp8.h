@@ -46,7 +46,7 @@ extern "C" {
 /* source dtypes for the quantizers */
 #define IFX_DTYPE_BF16 0
 #define IFX_DTYPE_F32 1
-#define IFX_DTYPE_F16 2 /* outputs of ifx_qkv_split only */
+#define IFX_DTYPE_F16 2 /* outputs of ifx_qkv_split; ifx_attention operands */
 
 /* activation selector for gated_act_quant (reference kernels/activation.py:15-16) */
 #define IFX_ACT_GELU_TANH 0
@@ -337,6 +337,34 @@ int ifx_fp8_pack_skinny(const void* w, int64_t ldw, int64_t N, int64_t K, void* 
  */
 int ifx_fp8_pack_glu(const void* w, const float* scale, const float* bias, int64_t F, int64_t K,
                      void* w_out, float* scale_out, float* bias_out, void* stream);
+
+/*
+ * Attention over q [B, Tq, Hq, D], k / v [B, Tk, Hkv, D] (dtype BF16 or F16,
+ * strides in elements given as {batch, token, head}, last dimension contiguous,
+ * multiples of 8; D % 8 == 0, D <= 256, Hq % Hkv == 0): grouped-query heads
+ * share their KV head (group = Hq / Hkv). Query token t sees keys [0, limit_t):
+ *   limit_t = kv_len (or kv_len_dev[0] read on the device when non-NULL)
+ *             + kv_extra[t] (int32 [Tq], when non-NULL)
+ *             then min(limit_t, t + causal_offset + 1) when causal,
+ *   clamped to the addressable keys (Tk, or n_index with kv_index).
+ * With kv_index (int32 [n_index]) key n is cache row kv_index[n].
+ * o [B, Tq, Hq, D] (o_strides) = softmax(q k^T * scale) v per head.
+ * splits > 1 spreads each row block's keys over `splits` workgroups, keeping
+ * partial softmax states in `workspace` (ifx_attention_workspace_size bytes, no
+ * zero-fill needed), then merges them; o may then be NULL, and with q8 != NULL
+ * (B == 1) every token's full output row [Hq * D] is also quantized per token to
+ * e4m3 q8 [Tq, ldq8] with q8_scale [Tq] (this package's recipe, as
+ * ifx_quant_rows). Hq * D <= 8192.
+ * Replaces: instinctflash/kernels/attention.py:159-213 `attention` (kernel :23-92,
+ * combine with fused FP8 output :113-147, SplitWorkspace :150-159).
+ */
+size_t ifx_attention_workspace_size(int64_t B, int64_t Tq, int64_t Hq, int64_t Hkv, int64_t D, int splits);
+int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B, int64_t Tq,
+                  int64_t Hq, int64_t Tk, int64_t Hkv, int64_t D, const int64_t* q_strides,
+                  const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides, int64_t kv_len,
+                  const int32_t* kv_len_dev, const int32_t* kv_extra, int causal, int64_t causal_offset,
+                  const int32_t* kv_index, int64_t n_index, float scale, int splits, void* workspace,
+                  size_t ws_bytes, void* q8, int64_t ldq8, float* q8_scale, void* stream);
 
 #ifdef __cplusplus
 }

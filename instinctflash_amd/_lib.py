@@ -77,6 +77,9 @@ SIGNATURES = {
     "ifx_residual_norm_quant": (_INT, [_P, _INT, _I64, _P, _INT, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _INT,
                                        ctypes.c_float, _P, _I64, _P, _P, _INT, _I64, _P, _P, _P, _I64, _INT,
                                        ctypes.c_float, _I64, _I64, _P]),
+    "ifx_attention_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _INT]),
+    "ifx_attention": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P,
+                             _INT, _I64, _P, _I64, ctypes.c_float, _INT, _P, _SZ, _P, _I64, _P, _P]),
     "ifx_moe_router": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _I64, _INT, ctypes.c_float, _P]),
     "ifx_moe_act_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "ifx_quant_linear": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64, _I64,

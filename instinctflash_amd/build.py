@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libifx_fp8.so"
-SOURCES = ("quant.hip", "gemm.hip", "norm.hip", "rope.hip")
+SOURCES = ("quant.hip", "gemm.hip", "norm.hip", "rope.hip", "attention.hip")
 ARCH = "gfx950"
 
 FLAGS = [

@@ -1,0 +1,108 @@
+"""Attention for short robotics sequences, with split-KV and a fused FP8
+output row, on HIP (gfx950).
+
+Mirrors instinctflash/kernels/attention.py: ``attention`` and ``SplitWorkspace``
+keep their signatures, so an engine's call sites run unchanged. Grouped-query
+heads fold into query rows; query token t sees keys [0, limit_t) with
+limit_t = kv_len (+ kv_extra[t]) (min causal_offset + t + 1); ``kv_len`` may be
+a one-element int32 device tensor read at execution time (captured graphs follow
+it); ``kv_index`` maps key n to cache row kv_index[n]. With ``split`` the keys
+of each row block are spread over several workgroups and merged by a second
+kernel, which can also emit every token's full output row as per-token E4M3
+(``q8``, ``q8_scale``) -- the A operand of the output projection.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from .fp8 import E4M3, _on_device, _ptr, _rows, _stream, _vec
+
+_DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+
+class SplitWorkspace:
+    """Partial-softmax storage for split-KV attention of one geometry
+    (reference attention.py:150-159). No initialization is needed."""
+
+    def __init__(self, batch, tq, hq, hkv, head_dim, splits, device):
+        self.splits = int(splits)
+        if self.splits < 2:
+            raise ValueError("a split workspace needs splits >= 2")
+        nbytes = _lib.load().ifx_attention_workspace_size(batch, tq, hq, hkv, head_dim, self.splits)
+        if nbytes == 0:
+            raise ValueError("unsupported split-attention geometry")
+        self.geometry = (int(batch), int(tq), int(hq), int(hkv), int(head_dim))
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def config_for(head_dim: int, group: int, rows: int):
+    """Launch choice of the reference's Triton kernel; the HIP kernel has one
+    configuration, so this only keeps the import surface (attention.py:103-106)."""
+    return (128, 64, 4, 1)
+
+
+def _strides(name, t, dev):
+    _on_device(name, t, dev)
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError(f"{name} must be 4-D with a contiguous last dimension")
+    return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+
+
+def attention(q, k, v, out=None, *, scale=None, kv_len=None, kv_extra=None, max_extra=0, causal=False,
+              causal_offset=0, config=None, tc5=False, split=None, q8=None, q8_scale=None, kv_index=None):
+    """Attention of q [B, Tq, Hq, D] over k / v [B, Tk, Hkv, D] (bf16 or fp16).
+
+    Reference: instinctflash/kernels/attention.py:162-213 (same keywords;
+    ``config`` and ``tc5`` select Triton launch shapes there and are accepted
+    and ignored here; ``max_extra`` only bounds ``kv_extra``). Returns ``out``
+    (allocated like q when omitted, unless a split launch writes only q8)."""
+    if q.dtype not in _DT or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share a dtype, bf16 or fp16")
+    dev = q.device
+    B, Tq, Hq, D = q.shape
+    if k.dim() != 4 or v.shape != k.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("k and v must be [B, Tk, Hkv, D] matching q")
+    Tk, Hkv = k.shape[1], k.shape[2]
+    if Hq % Hkv:
+        raise ValueError("query heads must be a multiple of KV heads")
+    if out is None and (split is None or q8 is None):
+        out = torch.empty_like(q)
+    if out is not None and (out.dtype != q.dtype or out.shape != q.shape):
+        raise ValueError("out must match q in shape and dtype")
+    qs, ks, vs = _strides("q", q, dev), _strides("k", k, dev), _strides("v", v, dev)
+    os_ = _strides("out", out, dev) if out is not None else None
+    if scale is None:
+        scale = D ** -0.5
+    dynamic = torch.is_tensor(kv_len)
+    if dynamic:
+        _vec("kv_len", kv_len, 1, dtype=torch.int32, device=dev)
+    static_len = Tk if kv_len is None or dynamic else int(kv_len)
+    if kv_index is not None:
+        _on_device("kv_index", kv_index, dev)
+        if kv_index.dtype != torch.int32 or kv_index.dim() != 1 or not kv_index.is_contiguous():
+            raise ValueError("kv_index must be a contiguous int32 vector")
+    _vec("kv_extra", kv_extra, Tq, dtype=torch.int32, device=dev)
+    splits, ws, ws_bytes = 1, None, 0
+    if split is not None:
+        if split.geometry != (B, Tq, Hq, Hkv, D):
+            raise ValueError(f"split workspace geometry {split.geometry} does not match {(B, Tq, Hq, Hkv, D)}")
+        splits, ws, ws_bytes = split.splits, split.buf, split.buf.numel()
+    ldq8 = 0
+    if q8 is not None:
+        if split is None:
+            raise ValueError("the fused FP8 output needs a split workspace")
+        if B != 1:
+            raise ValueError("fused FP8 output supports batch 1")
+        _, _, ldq8 = _rows("q8", q8, E4M3, dev, cols=Hq * D)
+        if q8.shape[0] != Tq:
+            raise ValueError(f"q8 must have {Tq} rows")
+        _vec("q8_scale", q8_scale, Tq, device=dev)
+    _lib.check(_lib.load().ifx_attention(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _DT[q.dtype], B, Tq, Hq, Tk, Hkv, D, qs, ks, vs, os_, static_len,
+        _ptr(kv_len) if dynamic else None, _ptr(kv_extra), 1 if causal else 0, int(causal_offset), _ptr(kv_index),
+        kv_index.numel() if kv_index is not None else 0, float(scale), splits, _ptr(ws), ws_bytes, _ptr(q8), ldq8,
+        _ptr(q8_scale), _stream(dev)), "ifx_attention")
+    return out

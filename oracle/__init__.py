@@ -43,6 +43,13 @@ Parts
     not weights); moe_act by the reference test's repeat_interleave
     construction of the column weights (:193-203), by reduction to the plain
     SwiGLU with unit weights, and by linearity in the routing weight.
+  * attention: softmax attention with per-row key limits (kernels/attention.py:
+    23-92, split combine :113-147) in float64. Pinned by the reference test's
+    own formulation (tests/test_gi_kernels.py:22-30: repeat_interleave of KV
+    heads, einsum, masked softmax) evaluated with torch, by
+    torch.nn.functional.scaled_dot_product_attention with a boolean mask, and by
+    closed forms (one visible key returns its value row; equal scores return
+    the mean of the visible value rows).
 """
 from __future__ import annotations
 
@@ -389,3 +396,30 @@ def moe_act(gu, row, col, route_w, experts, group, n_routed):
     grp = np.minimum(cols // group, experts - 1)
     wr = np.where(cols[None, :] < n_routed, np.asarray(route_w, f32)[:, grp], f32(1.0)).astype(f32)
     return ((silu(g.astype(f32)) * u).astype(f32) * wr).astype(f32)
+
+
+def attention(q, k, v, limits, scale, kv_index=None):
+    """Attention of instinctflash/kernels/attention.py:23-92, restated in float64.
+
+    q [B, Tq, Hq, D], k / v [B, Tk, Hkv, D] (any float dtype; Hq = group * Hkv,
+    query head h reads KV head h // group); limits int [Tq]: token t sees keys
+    [0, limits[t]); with kv_index key n is row kv_index[n] of k / v. Returns
+    float64 [B, Tq, Hq, D] = softmax(q . k^T * scale) . v over the visible keys."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    if kv_index is not None:
+        idx = np.asarray(kv_index, np.int64)
+        k, v = k[:, idx], v[:, idx]
+    B, Tq, Hq, D = q.shape
+    g = Hq // k.shape[2]
+    kk = np.repeat(k, g, axis=2)
+    vv = np.repeat(v, g, axis=2)
+    s = np.einsum("bqhd,bkhd->bhqk", q, kk) * scale
+    n = np.arange(kk.shape[1])
+    visible = n[None, :] < np.asarray(limits)[:, None]
+    s = np.where(visible[None, None], s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(axis=-1, keepdims=True)
+    return np.einsum("bhqk,bkhd->bqhd", p, vv)

@@ -529,3 +529,48 @@ def test_moe_act_matches_reference_test_construction(oracle_mod):
     ratio = cl[:, E * G:] / np.where(plain[:, E * G:] == 0, 1, plain[:, E * G:])
     nz = plain[:, E * G:] != 0
     assert np.allclose(ratio[nz], np.broadcast_to(rw.numpy()[:, E - 1:E], ratio.shape)[nz], rtol=1e-6)
+
+
+def _ref_attention_torch(q, k, v, limits, scale):
+    # tests/test_gi_kernels.py:22-30, evaluated in float64
+    g = q.shape[2] // k.shape[2]
+    kk = k.double().repeat_interleave(g, 2)
+    vv = v.double().repeat_interleave(g, 2)
+    s = torch.einsum("bqhd,bkhd->bhqk", q.double(), kk) * scale
+    n = torch.arange(k.shape[1])
+    s = s.masked_fill(~(n[None, :] < limits[:, None])[None, None], float("-inf"))
+    return torch.einsum("bhqk,bkhd->bqhd", s.softmax(-1), vv)
+
+
+@pytest.mark.parametrize("hd,hq,hkv", [(256, 8, 1), (72, 16, 16), (128, 16, 2)])
+def test_attention_matches_reference_formulation_and_sdpa(oracle_mod, hd, hq, hkv):
+    g = torch.Generator().manual_seed(hd)
+    q = torch.randn(2, 9, hq, hd, generator=g)
+    k = torch.randn(2, 21, hkv, hd, generator=g)
+    v = torch.randn(2, 21, hkv, hd, generator=g)
+    lim = torch.tensor([1, 5, 21, 13, 7, 21, 2, 3, 20])
+    got = oracle_mod.attention(q.numpy(), k.numpy(), v.numpy(), lim.numpy(), hd ** -0.5)
+    ref = _ref_attention_torch(q, k, v, lim, hd ** -0.5)
+    assert np.abs(got - ref.numpy()).max() < 1e-12
+    # torch's fused attention with the same boolean mask, per KV-head group
+    grp = hq // hkv
+    mask = torch.arange(21)[None, :] < lim[:, None]
+    sd = torch.nn.functional.scaled_dot_product_attention(
+        q.double().transpose(1, 2), k.double().repeat_interleave(grp, 2).transpose(1, 2),
+        v.double().repeat_interleave(grp, 2).transpose(1, 2), attn_mask=mask[None, None], scale=hd ** -0.5)
+    assert np.abs(got - sd.transpose(1, 2).numpy()).max() < 1e-10
+
+
+def test_attention_closed_forms_and_index(oracle_mod):
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((1, 4, 2, 16))
+    k = rng.standard_normal((1, 9, 1, 16))
+    v = rng.standard_normal((1, 9, 1, 16))
+    one = oracle_mod.attention(q, k, v, np.array([1, 1, 1, 1]), 0.25)
+    assert np.allclose(one, np.broadcast_to(v[:, :1], one.shape))  # one visible key: its value row
+    flat = oracle_mod.attention(np.zeros_like(q), k, v, np.array([3, 9, 5, 2]), 0.25)
+    for t, n in enumerate((3, 9, 5, 2)):  # equal scores: the mean of the visible rows
+        assert np.allclose(flat[0, t], v[0, :n, 0].mean(0)[None, :])
+    idx = np.array([8, 0, 4, 4, 2])  # pooled cache: key n is row idx[n]
+    got = oracle_mod.attention(q, k, v, np.array([5, 3, 1, 5]), 0.25, kv_index=idx)
+    assert np.allclose(got, oracle_mod.attention(q, k[:, idx], v[:, idx], np.array([5, 3, 1, 5]), 0.25))
