@@ -35,6 +35,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, TFLOP/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "FP8 linear TFLOP/s (% of MI355X FP8 MFMA peak) + GB/s for M<=64; p50 us/call"
 
 
@@ -139,10 +140,12 @@ def summarize(wl, m):
 
 
 def measure_producers(dev, launches=32):
-    """The row kernels around the projections: the pre-norm producer (residual
-    update + LayerNorm + adaLN + per-token quant) at the C5 and C2 shapes and the
-    QKV split consumer at the C4 shape: µs per call (graph of back-to-back calls,
-    median of 5) and GB/s of algorithmic bytes against the 8 TB/s roofline."""
+    """The kernels around the projections: the pre-norm producer (residual
+    update + LayerNorm + adaLN + per-token quant) at the C5 and C2 shapes, the
+    QKV split / Wan QKV consumers, the MoE router and routed activation, and
+    attention with the fused FP8 output row: µs per call (graph of back-to-back
+    calls, median of 5), GB/s of algorithmic bytes against the 8 TB/s roofline
+    and, for attention, TFLOP/s against the 2.5 PFLOP/s bf16 peak."""
     import torch
     from instinctflash_amd.workloads import CONSUMERS, PRODUCERS, NormQuant
     res = {}
@@ -162,6 +165,9 @@ def measure_producers(dev, launches=32):
         gbs = p.bytes / us / 1e3
         res[key] = {"kernel": p.title, "us": round(us, 3), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                     "bytes": p.bytes}
+        if hasattr(p, "flops"):  # bf16 matrix-core work (attention)
+            tf = p.flops / us / 1e6
+            res[key].update(tflops=round(tf, 2), frac_bf16_mfma=round(tf / BF16_PEAK_TFLOPS, 4))
         _log(f"[bench] {key}: {p.title}: {us:.2f} us, {gbs:.0f} GB/s")
     return res
 

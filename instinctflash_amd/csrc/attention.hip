@@ -140,7 +140,6 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
   const int split = blockIdx.y % a.splits;
   const int64_t b = blockIdx.z;
   const int D = static_cast<int>(a.D);
-  const int d16 = (D + 15) / 16;
 
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + wave * 32 + col;
   const bool row_ok = row < a.n_rows;
@@ -175,11 +174,11 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
   }
 
   // Q^T fragments (MFMA B operand): query `col`, dims 16c + 8*half .. +7
-  u32x4_t qf[(kDP + 15) / 16];
+  u32x4_t qf[2 * DT];
 #pragma unroll
-  for (int c = 0; c < (kDP + 15) / 16; ++c) {
+  for (int c = 0; c < 2 * DT; ++c) {
     const int d = 16 * c + 8 * half;
-    if (c < d16 && row_ok && d < D)
+    if (row_ok && d < D)
       qf[c] = *reinterpret_cast<const u32x4_t*>(a.q + b * a.sqb + tok * a.sqt + head * a.sqh + d);
     else
       qf[c] = u32x4_t{0u, 0u, 0u, 0u};
@@ -230,32 +229,34 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
     }
   };
 
-#ifndef IFX_ATT_DBG_NO_STAGE
-  if (start < end) fetch(start);
+  // Heads over 128 dims have no registers to spare for the next block's data:
+  // they load each block right before staging it.
+#ifndef IFX_ATT_PREFETCH_MAX_DT
+#define IFX_ATT_PREFETCH_MAX_DT 4
 #endif
+  constexpr bool kPrefetch = DT <= IFX_ATT_PREFETCH_MAX_DT;
+  if (kPrefetch && start < end) fetch(start);
   for (int n0 = start; n0 < end; n0 += kBlockN) {
-#ifndef IFX_ATT_DBG_NO_STAGE
+    if (!kPrefetch) fetch(n0);
     stage(n0);
-#endif
     __syncthreads();
-#ifndef IFX_ATT_DBG_NO_STAGE
-    if (n0 + kBlockN < end) fetch(n0 + kBlockN);
-#endif
+    if (kPrefetch && n0 + kBlockN < end) fetch(n0 + kBlockN);
 
     // ---- S^T = K . Q^T for the two 32-key tiles (two independent MFMA chains)
     v16f s[2] = {v16f{}, v16f{}};
+    // all 2 * DT chunks of the padded head: dims past D are zero in Q and K
 #pragma unroll
-    for (int c = 0; c < (kDP + 15) / 16; ++c) {
-      if (c < d16) {
+    for (int c = 0; c < 2 * DT; ++c) {
+      // at most 4 chunks of K fragments in registers ahead of their MFMAs
+      if (c % 4 == 0) asm volatile("" ::: "memory");
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lds + (32 * t + col) * kKPitch + 16 * c + 8 * half);
+      for (int t = 0; t < 2; ++t) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lds + (32 * t + col) * kKPitch + 16 * c + 8 * half);
 #ifndef IFX_ATT_DBG_NO_QK
-          s[t] = MF::run(kf, qf[c], s[t]);
+        s[t] = MF::run(kf, qf[c], s[t]);
 #else
-          s[t][0] += __uint_as_float(kf[0]);
+        s[t][0] += __uint_as_float(kf[0]);
 #endif
-        }
       }
     }
     // ---- online softmax (log2 domain); lane holds keys n0 + 32t + 8q + 4*half + r
@@ -314,6 +315,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int qp = 0; qp < 2; ++qp) {
+          if (DT > 4) asm volatile("" ::: "memory");  // bound the V fragments read ahead (registers)
           const u32x4_t pf = u32x4_t{pk[t][qp][0], pk[t][qp][1], pk[t][qp][2], pk[t][qp][3]};
           const uint16_t* vbk = v_lds + (32 * t + 16 * qp + vr) * kVPitch + vc;
 #pragma unroll
@@ -385,16 +387,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   auto prow_of = [&](int s, int64_t h) {
     return ((s * nb + b) * a.Hkv + h / a.group) * a.n_rows + tok * a.group + h % a.group;
   };
-  // per head: max over splits, then the normalized split weights
+  // the (head, split) softmax states in LDS, one load per thread, then per head
+  // the max over splits and the normalized split weights
+  __shared__ float pl_s[kCombineMaxW];
+  for (int64_t i = threadIdx.x; i < Hq * S; i += kAttnThreads) {
+    const int64_t pr = prow_of(static_cast<int>(i % S), i / S);
+    wgt[i] = a.pm[pr];
+    pl_s[i] = a.pl[pr];
+  }
+  __syncthreads();
   for (int64_t h = threadIdx.x; h < Hq; h += kAttnThreads) {
     float m = -__builtin_inff();
-    for (int s = 0; s < S; ++s) m = fmaxf(m, a.pm[prow_of(s, h)]);
+    for (int s = 0; s < S; ++s) m = fmaxf(m, wgt[h * S + s]);
     float l = 0.0f;
     for (int s = 0; s < S; ++s) {
-      const int64_t pr = prow_of(s, h);
-      const float w = __builtin_amdgcn_exp2f(a.pm[pr] - m);
+      const float w = __builtin_amdgcn_exp2f(wgt[h * S + s] - m);
       wgt[h * S + s] = w;
-      l = l + w * a.pl[pr];
+      l = l + w * pl_s[h * S + s];
     }
     const float inv = 1.0f / l;
     for (int s = 0; s < S; ++s) wgt[h * S + s] = wgt[h * S + s] * inv;

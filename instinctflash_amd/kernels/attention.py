@@ -38,6 +38,27 @@ class SplitWorkspace:
         self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
+_AUTO_SPLIT: dict = {}
+
+
+def _auto_split(B, Tq, Hq, Hkv, D, Tk, device):
+    """Split workspace for launches with too few row blocks to fill the GPU
+    (fewer than 128 workgroups of 128 query rows) over enough keys to split:
+    2..8 key ranges of >= 128 keys. Allocated once per geometry and device,
+    then reused (calls on one device are stream-ordered by the caller)."""
+    blocks = -(-(Tq * (Hq // Hkv)) // 128) * Hkv * B
+    if blocks >= 128 or Tk < 256:
+        return None
+    splits = int(min(8, max(2, 256 // blocks), Tk // 128))
+    if splits < 2:
+        return None
+    key = (device, B, Tq, Hq, Hkv, D, splits)
+    ws = _AUTO_SPLIT.get(key)
+    if ws is None:
+        ws = _AUTO_SPLIT[key] = SplitWorkspace(B, Tq, Hq, Hkv, D, splits, device)
+    return ws
+
+
 def config_for(head_dim: int, group: int, rows: int):
     """Launch choice of the reference's Triton kernel; the HIP kernel has one
     configuration, so this only keeps the import surface (attention.py:103-106)."""
@@ -58,7 +79,10 @@ def attention(q, k, v, out=None, *, scale=None, kv_len=None, kv_extra=None, max_
     Reference: instinctflash/kernels/attention.py:162-213 (same keywords;
     ``config`` and ``tc5`` select Triton launch shapes there and are accepted
     and ignored here; ``max_extra`` only bounds ``kv_extra``). Returns ``out``
-    (allocated like q when omitted, unless a split launch writes only q8)."""
+    (allocated like q when omitted, unless a split launch writes only q8).
+    Without ``split``, a launch with too few query-row blocks to fill the GPU
+    splits its keys anyway, through a workspace this module allocates once
+    per geometry."""
     if q.dtype not in _DT or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k and v must share a dtype, bf16 or fp16")
     dev = q.device
@@ -86,6 +110,8 @@ def attention(q, k, v, out=None, *, scale=None, kv_len=None, kv_extra=None, max_
             raise ValueError("kv_index must be a contiguous int32 vector")
     _vec("kv_extra", kv_extra, Tq, dtype=torch.int32, device=dev)
     splits, ws, ws_bytes = 1, None, 0
+    if split is None and q8 is None:
+        split = _auto_split(B, Tq, Hq, Hkv, D, Tk, dev)
     if split is not None:
         if split.geometry != (B, Tq, Hq, Hkv, D):
             raise ValueError(f"split workspace geometry {split.geometry} does not match {(B, Tq, Hq, Hkv, D)}")

@@ -538,5 +538,47 @@ class MoeAct:
                              group=self.G, n_routed=self.E * self.G)
 
 
+class Attn:
+    """``attention`` at the pi05 shapes (8 query heads, 1 KV head of 256 dims):
+    the 51-token action chunk over an 800-token prefix plus itself, split over
+    8 key ranges with the fused per-token E4M3 output row (the o-projection's A
+    operand), or the 800-token prefix self-attention. Work: 4 * Tq * Hq * Tk * D
+    FLOP (bf16 matrix cores); algorithmic bytes: q, k, v read once, the output
+    (bf16 row, or e4m3 row + scale) written once."""
+
+    def __init__(self, dev, Tq=51, Tk=851, Hq=8, Hkv=1, D=256, splits=8, q8=True, seed=0):
+        from .kernels.attention import SplitWorkspace, attention
+        self.attention, self.Tq, self.Tk, self.Hq, self.Hkv, self.D = attention, Tq, Tk, Hq, Hkv, D
+        g = _gen(seed)
+        self.q = torch.randn(1, Tq, Hq, D, generator=g).to(torch.bfloat16).to(dev)
+        self.k = torch.randn(1, Tk, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
+        self.v = torch.randn(1, Tk, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
+        self.ws = SplitWorkspace(1, Tq, Hq, Hkv, D, splits, dev) if splits > 1 else None
+        self.q8 = torch.empty(Tq, Hq * D, dtype=F.E4M3, device=dev) if q8 else None
+        self.qs = torch.empty(Tq, dtype=torch.float32, device=dev) if q8 else None
+        self.out = None if q8 else torch.empty_like(self.q)
+        kind = f"split {splits}, fused e4m3 row" if q8 else "bf16 out"
+        self.title = f"attention {Tq}x{Tk} keys, {Hq}/{Hkv} heads x {D} ({kind})"
+
+    @property
+    def flops(self) -> float:
+        return 4.0 * self.Tq * self.Hq * self.Tk * self.D
+
+    @property
+    def bytes(self) -> int:
+        qo = self.Tq * self.Hq * self.D
+        out = qo + 4 * self.Tq if self.q8 is not None else 2 * qo
+        return 2 * qo + 2 * 2 * self.Tk * self.Hkv * self.D + out
+
+    def step(self, i=0):
+        self.attention(self.q, self.k, self.v, out=self.out, split=self.ws, q8=self.q8, q8_scale=self.qs)
+
+
+class AttnPrefix(Attn):
+    def __init__(self, dev):
+        super().__init__(dev, Tq=800, Tk=800, splits=1, q8=False)
+
+
 PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}
-CONSUMERS = {"C4": QkvSplit, "C5": WanQkv, "vla2 MoE": MoeRoute, "vla2 MoE act": MoeAct}
+CONSUMERS = {"C4": QkvSplit, "C5": WanQkv, "vla2 MoE": MoeRoute, "vla2 MoE act": MoeAct, "pi05 chunk": Attn,
+             "pi05 prefix": AttnPrefix}
