@@ -172,6 +172,34 @@ def measure_producers(dev, launches=32):
     return res
 
 
+def measure_engine(dev, reps=5):
+    """The pi05 action expert end to end on these kernels (reference
+    engines/pi05/engine.py:212-245): 10 Euler steps x 18 layers over an
+    800-row prefix cache, random weights of the architecture, one captured
+    graph; ms per 50-action chunk (median of `reps` replays)."""
+    import torch
+    from instinctflash_amd.pi05 import Pi05Expert, random_weights
+    w = random_weights(dev, layers=18, steps=10, seed=0)
+    eng = Pi05Expert(w, dev, smax=832)
+    g = torch.Generator().manual_seed(1)
+    eng.kc[:, :800] = torch.randn(18, 800, 1, 256, generator=g).half().to(dev)
+    eng.vc[:, :800] = torch.randn(18, 800, 1, 256, generator=g).half().to(dev)
+    eng.set_prefix(800)
+    eng.noise.copy_(torch.randn(eng.chunk, 32, generator=g))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eng.forward()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = capture(lambda i: eng.forward(), 1, side)
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    launches = 10 * (2 + 18 * 10)
+    _log(f"[bench] pi05 expert: {ms:.3f} ms per 50-action chunk ({launches} kernels + torch addmm)")
+    return {"workload": "pi05 action expert, 10 steps x 18 layers, prefix 800, chunk 50 (random weights)",
+            "ms_per_chunk": round(ms, 4), "kernels_per_chunk": launches}
+
+
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -337,6 +365,7 @@ def main():
     }
     if not args.no_others:
         out["producers"] = measure_producers(dev)
+        out["engine"] = measure_engine(dev)
     if not args.no_cpu:
         _log("[bench] CPU baseline (reference CPU FP8 path, one C2 unit)")
         out["cpu_baseline"] = cpu_baseline()

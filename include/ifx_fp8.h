@@ -117,15 +117,21 @@ int ifx_quant_tensor_bf16(const void* x, int64_t count, void* q, float* scale, v
  */
 int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void* q, void* stream);
 
+/* Flags of ifx_row_quant. */
+#define IFX_RQ_GELU 1 /* gelu_tanh after the affine terms */
+#define IFX_RQ_F16 2  /* x holds fp16 (default bf16) */
+
 /*
- * Consumer-side producer of the next FP8 operand from a raw bf16 accumulator:
+ * Consumer-side producer of the next FP8 operand from a raw bf16 (or fp16)
+ * accumulator:
  *   v = x[m,k] * row[m] * col[k] + bias[k]   (NULL factors are skipped)
- *   v = gelu_tanh(v) if gelu
+ *   v = gelu_tanh(v) with IFX_RQ_GELU
  *   (q[m,:], scale[m]) = quantize(v) with the recipe above (FP32 v, no bf16 rounding).
- * Replaces: instinctflash/kernels/norm.py:150-158 `row_quant`.
+ * Replaces: instinctflash/kernels/norm.py:150-158 `row_quant` (which the pi05
+ * engine also applies to its fp16 attention output, engines/pi05/engine.py:205).
  */
 int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row,
-                  const float* col, const float* bias, int gelu, void* q, int64_t ldq,
+                  const float* col, const float* bias, int flags, void* q, int64_t ldq,
                   float* scale, void* stream);
 
 /*

@@ -27,6 +27,9 @@ DTYPE_BF16 = 0
 DTYPE_F32 = 1
 DTYPE_F16 = 2
 
+RQ_GELU = 1
+RQ_F16 = 2
+
 ACT_GELU_TANH = 0
 ACT_SILU = 1
 

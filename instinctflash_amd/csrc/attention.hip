@@ -281,7 +281,11 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
         }
     }
     mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
-    const float m_new = fmaxf(m_run, mblk);
+    // The reference max only moves when a score exceeds it by more than 2^8
+    // (probabilities then stay <= 256, exact in the 16-bit P operand's range),
+    // so the accumulators are rarely rescaled; l and O share the reference, so
+    // the normalized result is the same.
+    const float m_new = mblk > m_run + 8.0f ? fmaxf(m_run, mblk) : m_run;
     const float m_use = m_new == -__builtin_inff() ? 0.0f : m_new;
     float psum = 0.0f;
     uint32_t pk[2][2][4];  // [tile][q0 pair][packed pairs]
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
         psum = psum + p0 + p1;
         pk[t][i >> 3][(i & 7) >> 1] = MF::pack2(p0, p1);
       }
-    // rescale only when some row's running max grew (the rescale is by 1 otherwise)
+    // rescale only when some row's reference moved (the rescale is by 1 otherwise)
     if (__any(m_new != m_run)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       l_run = l_run * alpha;
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
 // weights exp2(m_s - m) / l are formed once in LDS; the row's values stay in
 // registers between the two passes (Hq * D <= 256 * kCombineVpt).
 constexpr int kCombineVpt = 32;
-constexpr int kCombineMaxW = 4096;  // Hq * splits
+constexpr int kCombineMaxW = 1024;  // Hq * splits
 
 template <bool BF16>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, int64_t kdp, int64_t Hq,
@@ -383,51 +387,69 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   const int64_t tok = blockIdx.y;
   const int D = static_cast<int>(a.D);
   const int S = a.splits;
+  const int H = static_cast<int>(Hq);
   const int64_t nb = gridDim.x;
-  auto prow_of = [&](int s, int64_t h) {
-    return ((s * nb + b) * a.Hkv + h / a.group) * a.n_rows + tok * a.group + h % a.group;
-  };
-  // the (head, split) softmax states in LDS, one load per thread, then per head
-  // the max over splits and the normalized split weights
+  // per (head, split): the partial row's index, its softmax state in LDS
   __shared__ float pl_s[kCombineMaxW];
-  for (int64_t i = threadIdx.x; i < Hq * S; i += kAttnThreads) {
-    const int64_t pr = prow_of(static_cast<int>(i % S), i / S);
+  __shared__ int64_t off_s[kCombineMaxW];
+  for (int i = threadIdx.x; i < H * S; i += kAttnThreads) {
+    const int h = i / S, sp = i - (i / S) * S;
+    const int64_t pr = ((sp * nb + b) * a.Hkv + h / a.group) * a.n_rows + tok * a.group + h % a.group;
+    off_s[i] = pr * kdp;
     wgt[i] = a.pm[pr];
     pl_s[i] = a.pl[pr];
   }
   __syncthreads();
-  for (int64_t h = threadIdx.x; h < Hq; h += kAttnThreads) {
+  // per head: the max over splits, then the normalized split weights
+  for (int h = threadIdx.x; h < H; h += kAttnThreads) {
     float m = -__builtin_inff();
-    for (int s = 0; s < S; ++s) m = fmaxf(m, wgt[h * S + s]);
+    for (int sp = 0; sp < S; ++sp) m = fmaxf(m, wgt[h * S + sp]);
     float l = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float w = __builtin_amdgcn_exp2f(wgt[h * S + s] - m);
-      wgt[h * S + s] = w;
-      l = l + w * pl_s[h * S + s];
+    for (int sp = 0; sp < S; ++sp) {
+      const float w = __builtin_amdgcn_exp2f(wgt[h * S + sp] - m);
+      wgt[h * S + sp] = w;
+      l = l + w * pl_s[h * S + sp];
     }
     const float inv = 1.0f / l;
-    for (int s = 0; s < S; ++s) wgt[h * S + s] = wgt[h * S + s] * inv;
+    for (int sp = 0; sp < S; ++sp) wgt[h * S + sp] = wgt[h * S + sp] * inv;
   }
   __syncthreads();
-  const int64_t width = Hq * D;
-  float val[kCombineVpt];
+  // the merged row in groups of 4 head dims; the partials of up to 16 splits of
+  // a group are loaded together (addresses clamped, weights zeroed past S)
+  constexpr int kG = kCombineVpt / 4;  // groups per thread
+  const int groups = H * D / 4;
+  float4 val[kG];
   uint32_t amax = 0;
 #pragma unroll
-  for (int j = 0; j < kCombineVpt; ++j) {
-    const int64_t e = threadIdx.x + static_cast<int64_t>(j) * kAttnThreads;
-    val[j] = 0.0f;
-    if (e >= width) continue;
-    const int64_t h = e / D, d = e % D;
-    float out = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) out = out + wgt[h * S + s] * a.po[prow_of(s, h) * kdp + d];
-    val[j] = out;
-    if (a.o) {
-      const uint32_t p = MF::pack2(out, 0.0f);
-      a.o[b * a.sob + tok * a.sot + h * a.soh + d] = static_cast<uint16_t>(p & 0xFFFFu);
+  for (int j = 0; j < kG; ++j) {
+    const int e4 = threadIdx.x + j * kAttnThreads;
+    val[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e4 >= groups) continue;
+    const int h = (4 * e4) / D, d = 4 * e4 - h * D;
+    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < S; s0 += 16) {
+      float4 pv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int sp = min(s0 + u, S - 1);
+        pv[u] = *reinterpret_cast<const float4*>(a.po + off_s[h * S + sp] + d);
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float w = s0 + u < S ? wgt[h * S + s0 + u] : 0.0f;
+        o4.x = o4.x + w * pv[u].x;
+        o4.y = o4.y + w * pv[u].y;
+        o4.z = o4.z + w * pv[u].z;
+        o4.w = o4.w + w * pv[u].w;
+      }
     }
-    const uint32_t bits = abs_bits(out);
-    amax = amax > bits ? amax : bits;
+    val[j] = o4;
+    if (a.o) {
+      uint16_t* op = a.o + b * a.sob + tok * a.sot + h * a.soh + d;
+      *reinterpret_cast<uint2*>(op) = make_uint2(MF::pack2(o4.x, o4.y), MF::pack2(o4.z, o4.w));
+    }
+    const uint32_t m1 = max(abs_bits(o4.x), abs_bits(o4.y)), m2 = max(abs_bits(o4.z), abs_bits(o4.w));
+    amax = max(amax, max(m1, m2));
   }
   if (!q8) return;  // uniform
   amax = wave_max_u32(amax);
@@ -439,9 +461,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   const float sc = scale_from_amax_bits(amax);
   if (threadIdx.x == 0) q8s[tok] = sc;
 #pragma unroll
-  for (int j = 0; j < kCombineVpt; ++j) {
-    const int64_t e = threadIdx.x + static_cast<int64_t>(j) * kAttnThreads;
-    if (e < width) q8[tok * ldq8 + e] = static_cast<uint8_t>(q1(val[j], sc));
+  for (int j = 0; j < kG; ++j) {
+    const int e4 = threadIdx.x + j * kAttnThreads;
+    if (e4 < groups) {
+      uint8_t* qp = q8 + tok * ldq8 + 4 * e4;
+      qp[0] = static_cast<uint8_t>(q1(val[j].x, sc));
+      qp[1] = static_cast<uint8_t>(q1(val[j].y, sc));
+      qp[2] = static_cast<uint8_t>(q1(val[j].z, sc));
+      qp[3] = static_cast<uint8_t>(q1(val[j].w, sc));
+    }
   }
 }
 

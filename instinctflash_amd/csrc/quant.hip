@@ -99,7 +99,24 @@ struct SrcAffine {
   const float* col;
   const float* bias;
   int gelu;
+  int f16;  // x holds fp16 (else bf16)
   struct Raw { uint4 a; Vec8 c, b; };
+  __device__ __forceinline__ void unpack(const uint4& r, float* v) const {
+    if (!f16) {
+      unpack_bf16x8(r, v);
+      return;
+    }
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xFFFFu)));
+      v[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+    }
+  }
+  __device__ __forceinline__ float elem(int64_t m, int64_t k) const {
+    const uint16_t h = x[m * ldx + k];
+    return f16 ? static_cast<float>(__builtin_bit_cast(_Float16, h)) : bf16_bits_to_f32(h);
+  }
   __device__ __forceinline__ float op(float v, float r, float c, float b) const {
     if (row) v = v * r;
     if (col) v = v * c;
@@ -114,12 +131,12 @@ struct SrcAffine {
     if constexpr (HB) r.b.load(bias + k);
   }
   __device__ __forceinline__ void finish(const Raw& r, float rs, int64_t, int64_t, float* v) const {
-    unpack_bf16x8(r.a, v);
+    unpack(r.a, v);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = op(v[i], rs, HC ? r.c[i] : 1.0f, HB ? r.b[i] : 0.0f);
   }
   __device__ __forceinline__ float load1(int64_t m, int64_t k) const {
-    return op(bf16_bits_to_f32(x[m * ldx + k]), row ? row[m] : 1.0f, col ? col[k] : 1.0f, bias ? bias[k] : 0.0f);
+    return op(elem(m, k), row ? row[m] : 1.0f, col ? col[k] : 1.0f, bias ? bias[k] : 0.0f);
   }
 };
 
@@ -596,9 +613,10 @@ int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void*
 }
 
 int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row,
-                  const float* col, const float* bias, int gelu, void* q, int64_t ldq,
+                  const float* col, const float* bias, int flags, void* q, int64_t ldq,
                   float* scale, void* stream) {
   if (M < 0 || K < 0 || ldx < K || ldq < K) return IFX_ERR_INVALID;
+  if (flags & ~(IFX_RQ_GELU | IFX_RQ_F16)) return IFX_ERR_INVALID;
   if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
   const bool vec_ok = aligned16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 &&
                       aligned16(col) && aligned16(bias);
@@ -608,7 +626,8 @@ int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float*
     s.row = row;
     s.col = col;
     s.bias = bias;
-    s.gelu = gelu ? 1 : 0;
+    s.gelu = (flags & IFX_RQ_GELU) ? 1 : 0;
+    s.f16 = (flags & IFX_RQ_F16) ? 1 : 0;
     return dispatch_rows(s, vec_ok, M, K, static_cast<uint8_t*>(q), ldq, scale, static_cast<hipStream_t>(stream));
   };
   if (col) return bias ? go(SrcAffine<true, true>{}) : go(SrcAffine<true, false>{});

@@ -43,15 +43,14 @@ _AUTO_SPLIT: dict = {}
 
 def _auto_split(B, Tq, Hq, Hkv, D, Tk, device):
     """Split workspace for launches with too few row blocks to fill the GPU
-    (fewer than 128 workgroups of 128 query rows) over enough keys to split:
-    2..8 key ranges of >= 128 keys. Allocated once per geometry and device,
-    then reused (calls on one device are stream-ordered by the caller)."""
+    (fewer than 128 workgroups of 128 query rows): the keys are cut into ranges
+    of about 128 (2..16 ranges), so each workgroup's chain of dependent key
+    blocks stays short. Allocated once per geometry and device, then reused
+    (calls on one device are stream-ordered by the caller)."""
     blocks = -(-(Tq * (Hq // Hkv)) // 128) * Hkv * B
-    if blocks >= 128 or Tk < 256:
+    if blocks >= 128 or Tk < 256 or Hq * 16 > 1024:
         return None
-    splits = int(min(8, max(2, 256 // blocks), Tk // 128))
-    if splits < 2:
-        return None
+    splits = int(min(16, max(2, -(-Tk // 128))))
     key = (device, B, Tq, Hq, Hkv, D, splits)
     ws = _AUTO_SPLIT.get(key)
     if ws is None:

@@ -220,6 +220,26 @@ def test_row_quant_gelu(gpu, oracle_mod):
     assert err.max() < 0.07
 
 
+@pytest.mark.parametrize("M,D", [(50, 2048), (7, 520), (300, 1024)])
+def test_row_quant_fp16_input(gpu, oracle_mod, M, D):
+    # the pi05 engine quantizes its fp16 attention output (engines/pi05/engine.py:205):
+    # fp16 -> fp32 is exact, so bytes and scales are bit-exact to the oracle recipe
+    from instinctflash_amd.kernels import row_quant
+    g = torch.Generator().manual_seed(M + D)
+    x = (torch.randn((M, D), generator=g) * 2).to(torch.float16)
+    q = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    row_quant(x.to(gpu), q, s)
+    eq, es = oracle_mod.quant_rows(x.float().numpy())
+    assert np.array_equal(_q(q), eq) and np.array_equal(_f(s), es)
+    row = torch.rand(M, generator=g) + 0.5
+    col = torch.rand(D, generator=g) + 0.5
+    row_quant(x.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu))
+    v = (x.float().numpy() * row.numpy()[:, None]).astype(np.float32) * col.numpy()[None, :]
+    eq, es = oracle_mod.quant_rows(v.astype(np.float32))
+    assert np.array_equal(_q(q), eq) and np.array_equal(_f(s), es)
+
+
 @pytest.mark.parametrize("act", [0, 1])
 def test_gated_act_quant(gpu, oracle_mod, act):
     from instinctflash_amd.kernels import gated_act_quant
