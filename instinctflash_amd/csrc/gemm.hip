@@ -1201,7 +1201,10 @@ int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint
   return launch_status();
 }
 
-constexpr int64_t kSkinnyMaxM = 64;
+#ifndef IFX_SKINNY_MAX_M
+#define IFX_SKINNY_MAX_M 64
+#endif
+constexpr int64_t kSkinnyMaxM = IFX_SKINNY_MAX_M;
 
 // One thread per 16-byte chunk of the tiled layout: chunk c = ((b * ks + s) *
 // 2 + half) * 64 + l holds row 16b + l%16, K bytes s*128 + 32*(l/16) + 16*half
