@@ -117,6 +117,15 @@ int ifx_quant_tensor_bf16(const void* x, int64_t count, void* q, float* scale, v
  */
 int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void* q, void* stream);
 
+/*
+ * Row stride value selecting the skinny tile layout of ifx_quant_rows_tiled for
+ * the e4m3 output of ifx_row_quant, ifx_gated_act_quant, ifx_moe_act_quant,
+ * ifx_residual_norm_quant and ifx_attention's q8 (M <= 64 rows, K % 16 == 0,
+ * 16-byte aligned; ifx_quant_rows_tiled_bytes(M, K) bytes): the layout the
+ * M <= 64 GEMM reads with 1 KB contiguous loads (IFX_EPI_A_TILED).
+ */
+#define IFX_LD_TILED 0
+
 /* Flags of ifx_row_quant. */
 #define IFX_RQ_GELU 1 /* gelu_tanh after the affine terms */
 #define IFX_RQ_F16 2  /* x holds fp16 (default bf16) */

@@ -27,6 +27,8 @@ DTYPE_BF16 = 0
 DTYPE_F32 = 1
 DTYPE_F16 = 2
 
+LD_TILED = 0  # row stride selecting the skinny tile layout of an e4m3 output
+
 RQ_GELU = 1
 RQ_F16 = 2
 

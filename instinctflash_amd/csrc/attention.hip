@@ -377,9 +377,12 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
 constexpr int kCombineVpt = 32;
 constexpr int kCombineMaxW = 1024;  // Hq * splits
 
+// ks > 0: q8 in the skinny tile layout (ks K steps; the grid covers 16*ceil(Tq/16)
+// token rows and the padding rows / K padding are written as zeros).
 template <bool BF16>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, int64_t kdp, int64_t Hq,
-                                                                    uint8_t* q8, int64_t ldq8, float* q8s) {
+                                                                    uint8_t* q8, int64_t ldq8, float* q8s, int64_t ks,
+                                                                    int64_t Tq) {
   using MF = Mfma<BF16>;
   __shared__ uint32_t red[kAttnThreads / 64];
   __shared__ float wgt[kCombineMaxW];
@@ -388,6 +391,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   const int D = static_cast<int>(a.D);
   const int S = a.splits;
   const int H = static_cast<int>(Hq);
+  if (tok >= Tq) {  // tile-layout padding row (workgroup-uniform)
+    for (int64_t i = threadIdx.x; i < ks * 16; i += kAttnThreads)
+      *reinterpret_cast<uint2*>(q8 + tile_offset(tok, 8 * i, ks)) = make_uint2(0u, 0u);
+    return;
+  }
   const int64_t nb = gridDim.x;
   // per (head, split): the partial row's index, its softmax state in LDS
   __shared__ float pl_s[kCombineMaxW];
@@ -464,13 +472,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   for (int j = 0; j < kG; ++j) {
     const int e4 = threadIdx.x + j * kAttnThreads;
     if (e4 < groups) {
-      uint8_t* qp = q8 + tok * ldq8 + 4 * e4;
+      uint8_t* qp = ks > 0 ? q8 + tile_offset(tok, 4 * e4, ks) : q8 + tok * ldq8 + 4 * e4;
       qp[0] = static_cast<uint8_t>(q1(val[j].x, sc));
       qp[1] = static_cast<uint8_t>(q1(val[j].y, sc));
       qp[2] = static_cast<uint8_t>(q1(val[j].z, sc));
       qp[3] = static_cast<uint8_t>(q1(val[j].w, sc));
     }
   }
+  if (ks > 0)  // K padding of the tile layout
+    for (int64_t i = groups / 2 + threadIdx.x; i < ks * 16; i += kAttnThreads)
+      *reinterpret_cast<uint2*>(q8 + tile_offset(tok, 8 * i, ks)) = make_uint2(0u, 0u);
 }
 
 template <bool BF16, int DT>
@@ -522,7 +533,9 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
   if (kv_len < 0 || causal_offset < -(int64_t(1) << 30) || causal_offset > (int64_t(1) << 30) ||
       Tk > 0x7FFFFFFFLL || n_index > 0x7FFFFFFFLL)
     return IFX_ERR_INVALID;
-  if (q8 && (splits < 2 || B != 1 || !q8_scale || ldq8 < Hq * D)) return IFX_ERR_INVALID;
+  if (q8 && (splits < 2 || B != 1 || !q8_scale || (ldq8 != IFX_LD_TILED && ldq8 < Hq * D))) return IFX_ERR_INVALID;
+  const int64_t q8_ks = q8 && ldq8 == IFX_LD_TILED ? (Hq * D + 127) / 128 : 0;
+  if (q8_ks > 0 && (Tq > 64 || (Hq * D) % 16 != 0 || !aligned16(q8))) return IFX_ERR_UNSUPPORTED;
   if (Hq * D > static_cast<int64_t>(kAttnThreads) * kCombineVpt || Hq * splits > kCombineMaxW)
     return IFX_ERR_UNSUPPORTED;
   if (splits == 1 && !o) return IFX_ERR_INVALID;
@@ -578,13 +591,13 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
   if (bf) dispatch_attn<true>(a, B, dt, st);
   else dispatch_attn<false>(a, B, dt, st);
   if (splits > 1) {
-    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(Tq));
+    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(q8_ks > 0 ? (Tq + 15) / 16 * 16 : Tq));
     if (bf)
       hipLaunchKernelGGL((attn_combine_kernel<true>), grid, dim3(kAttnThreads), 0, st, a, int64_t(32 * dt), Hq,
-                         static_cast<uint8_t*>(q8), ldq8, q8_scale);
+                         static_cast<uint8_t*>(q8), ldq8, q8_scale, q8_ks, Tq);
     else
       hipLaunchKernelGGL((attn_combine_kernel<false>), grid, dim3(kAttnThreads), 0, st, a, int64_t(32 * dt), Hq,
-                         static_cast<uint8_t*>(q8), ldq8, q8_scale);
+                         static_cast<uint8_t*>(q8), ldq8, q8_scale, q8_ks, Tq);
   }
   return launch_status();
 }

@@ -70,6 +70,14 @@ __device__ __forceinline__ uint2 pack8_exact(const float* v, float s) {
   return o;
 }
 
+// Byte offset of element (m, k) (k % 8 == 0) in the skinny tile layout with ks
+// K steps per 16-row block: tile (m/16, k/128) of 2 KB, lane l = 16*((k%128)/32)
+// + m%16 holds K bytes [32*(l/16), +16) at 16l and the next 16 at 1024 + 16l.
+__device__ __forceinline__ int64_t tile_offset(int64_t m, int64_t k, int64_t ks) {
+  return ((m >> 4) * ks + (k >> 7)) * 2048 + ((k >> 4) & 1) * 1024 + ((((k >> 5) & 3) << 4) + (m & 15)) * 16 +
+         (k & 15);
+}
+
 __device__ __forceinline__ bool finite_scale(float s) { return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u; }
 
 }  // namespace ifx

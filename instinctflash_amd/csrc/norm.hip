@@ -70,6 +70,8 @@ struct RnqArgs {
   int flags;
   int y_f32;
   RouterArgs router;
+  int64_t M;
+  int64_t ks;  // > 0: q in the skinny tile layout with ks K steps (grid covers 16*ceil(M/16) rows)
 };
 
 __device__ __forceinline__ void load8_bf16(const void* p, float* v) {
@@ -294,6 +296,11 @@ __global__ __launch_bounds__(kRnqThreads) void residual_norm_quant_kernel(RnqArg
   __shared__ float logit[ROUTER ? kRouterMaxE : 1];
   __shared__ float wsl[ROUTER ? kRouterMaxE : 1];
   const int64_t row = blockIdx.x;
+  if (row >= a.M) {  // tile-layout padding row (workgroup-uniform): zeros only
+    for (int64_t idx = threadIdx.x; idx < a.ks * 16; idx += kRnqThreads)
+      *reinterpret_cast<uint2*>(a.q + tile_offset(row, idx * 8, a.ks)) = make_uint2(0u, 0u);
+    return;
+  }
   const int64_t D = a.D;
   const int64_t mofs = a.mod_index ? static_cast<int64_t>(a.mod_index[row]) * D : 0;
   const bool has_delta = a.delta != nullptr;
@@ -463,8 +470,12 @@ __global__ __launch_bounds__(kRnqThreads) void residual_norm_quant_kernel(RnqArg
     for (int j = 0; j < VPT; ++j) {
       if (!on[j]) continue;
       const int64_t c = (static_cast<int64_t>(j) * kRnqThreads + threadIdx.x) * 8;
-      *reinterpret_cast<uint2*>(a.q + row * a.ldq + c) = fast ? pack8_fast(x[j], s, r) : pack8_exact(x[j], s);
+      uint8_t* dst = a.ks > 0 ? a.q + tile_offset(row, c, a.ks) : a.q + row * a.ldq + c;
+      *reinterpret_cast<uint2*>(dst) = fast ? pack8_fast(x[j], s, r) : pack8_exact(x[j], s);
     }
+    if (a.ks > 0)  // K padding of the tile layout
+      for (int64_t idx = D / 8 + threadIdx.x; idx < a.ks * 16; idx += kRnqThreads)
+        *reinterpret_cast<uint2*>(a.q + tile_offset(row, idx * 8, a.ks)) = make_uint2(0u, 0u);
   }
   if constexpr (ROUTER != 0) {
     __syncthreads();
@@ -476,7 +487,7 @@ __global__ __launch_bounds__(kRnqThreads) void residual_norm_quant_kernel(RnqArg
 
 template <int VPT>
 void launch_rnq(const RnqArgs& a, int64_t M, bool res_bf16, bool delta_bf16, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(M)), block(kRnqThreads);
+  const dim3 grid(static_cast<unsigned>(a.ks > 0 ? (M + 15) / 16 * 16 : M)), block(kRnqThreads);
   const bool router = a.router.w != nullptr;
   const bool pf = router && VPT == 1 && router_prefetch_ok(a.router.E, a.D, a.router.w);
   const bool many = M >= 1024;
@@ -517,7 +528,7 @@ int ifx_residual_norm_quant(void* res, int res_dtype, int64_t ldres, const void*
   if (!dtype_ok(res_dtype) || (delta && !dtype_ok(delta_dtype)) || (y && !dtype_ok(y_dtype))) return IFX_ERR_INVALID;
   if (M < 0 || D <= 0 || D % 8 != 0) return IFX_ERR_INVALID;
   if (D > static_cast<int64_t>(kRnqThreads) * 8 * 8) return IFX_ERR_UNSUPPORTED;
-  if (ldres < D || (delta && lddelta < D) || (q && ldq < D) || (y && ldy < D)) return IFX_ERR_INVALID;
+  if (ldres < D || (delta && lddelta < D) || (q && ldq != IFX_LD_TILED && ldq < D) || (y && ldy < D)) return IFX_ERR_INVALID;
   if ((mod_scale == nullptr) != (mod_shift == nullptr)) return IFX_ERR_INVALID;
   if (q && !q_scale) return IFX_ERR_INVALID;
   if (!(eps >= 0.0f)) return IFX_ERR_INVALID;
@@ -537,7 +548,9 @@ int ifx_residual_norm_quant(void* res, int res_dtype, int64_t ldres, const void*
   RnqArgs a{res, ldres, delta, lddelta, delta_row, delta_col, bias, gate, weight, beta, mod_scale, mod_shift,
             mod_index, y, ldy, static_cast<uint8_t*>(q), ldq, q_scale, D, eps, delta ? flags : (flags & ~IFX_RNQ_WRITE_RES),
             y_dtype == IFX_DTYPE_F32 ? 1 : 0,
-            RouterArgs{router_w, router_bias, route_w, static_cast<int>(router_E), router_top_k, router_scale}};
+            RouterArgs{router_w, router_bias, route_w, static_cast<int>(router_E), router_top_k, router_scale}, M,
+            q && ldq == IFX_LD_TILED ? (D + 127) / 128 : 0};
+  if (a.ks > 0 && (M > 64 || D % 16 != 0 || !aligned16(q))) return IFX_ERR_UNSUPPORTED;
   const bool rb = res_dtype == IFX_DTYPE_BF16, db = delta_dtype == IFX_DTYPE_BF16;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t groups = (D / 8 + kRnqThreads - 1) / kRnqThreads;  // 8-element groups per lane

@@ -234,14 +234,6 @@ __device__ __forceinline__ uint32_t team_max(uint32_t v, uint32_t* red) {
 
 // Register-resident row quantizer: K % 8 == 0, 16-byte aligned rows,
 // ceil(K/8) <= T*VPT.
-// Byte offset of element (m, k) (k % 8 == 0) in the skinny tile layout with ks
-// K steps per 16-row block: tile (m/16, k/128) of 2 KB, lane l = 16*((k%128)/32)
-// + m%16 holds K bytes [32*(l/16), +16) at 16l and the next 16 at 1024 + 16l.
-__device__ __forceinline__ int64_t tile_offset(int64_t m, int64_t k, int64_t ks) {
-  return ((m >> 4) * ks + (k >> 7)) * 2048 + ((k >> 4) & 1) * 1024 + ((((k >> 5) & 3) << 4) + (m & 15)) * 16 +
-         (k & 15);
-}
-
 // ks == 0: q is row-major with stride ldq. ks > 0: q is the skinny tile layout
 // (rows M..16*ceil(M/16)-1 and K bytes K..128*ks-1 are written as zeros, by the
 // launch covering m_rows = 16*ceil(M/16) rows).
@@ -340,6 +332,8 @@ void launch_vec(const Src& src, int64_t M, int64_t K, uint8_t* q, int64_t ldq, f
 
 // Picks the register-resident variant (team size, vectors per lane) or falls
 // back to the two-pass kernel.
+// ldq == IFX_LD_TILED: q is the skinny tile layout of ifx_quant_rows_tiled
+// (M <= 64, K % 16 == 0, 16-byte aligned rows).
 template <class Src>
 int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q, int64_t ldq,
                   float* scale, hipStream_t st) {
@@ -349,6 +343,15 @@ int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q,
   }
   if (M > 0x7FFFFFFFLL) return IFX_ERR_INVALID;
   const int64_t nvec = K / 8;
+  if (ldq == IFX_LD_TILED) {
+    if (!vec_ok || K % 16 != 0 || M > 64 || nvec > 2048 || !aligned16(q)) return IFX_ERR_UNSUPPORTED;
+    const int64_t ks = (K + 127) / 128;
+    if (nvec <= 256) launch_vec<256, 1>(src, M, K, q, 0, scale, st, ks);
+    else if (nvec <= 512) launch_vec<512, 1, Src, 512>(src, M, K, q, 0, scale, st, ks);
+    else if (nvec <= 1024) launch_vec<1024, 1, Src, 1024>(src, M, K, q, 0, scale, st, ks);
+    else launch_vec<1024, 2, Src, 1024>(src, M, K, q, 0, scale, st, ks);
+    return launch_status();
+  }
   if (vec_ok && K % 8 == 0 && nvec <= 4096 && M < 256) {
     // Few rows: latency-bound, so give every row a whole 256-lane block
     // instead of packing rows per block; wide rows get up to 1024 lanes, so
@@ -615,7 +618,7 @@ int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void*
 int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float* row,
                   const float* col, const float* bias, int flags, void* q, int64_t ldq,
                   float* scale, void* stream) {
-  if (M < 0 || K < 0 || ldx < K || ldq < K) return IFX_ERR_INVALID;
+  if (M < 0 || K < 0 || ldx < K || (ldq != IFX_LD_TILED && ldq < K)) return IFX_ERR_INVALID;
   if (flags & ~(IFX_RQ_GELU | IFX_RQ_F16)) return IFX_ERR_INVALID;
   if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
   const bool vec_ok = aligned16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 &&
@@ -636,7 +639,7 @@ int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float*
 
 int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row,
                         const float* col, int act, void* q, int64_t ldq, float* scale, void* stream) {
-  if (M < 0 || F < 0 || ldgu < 2 * F || ldq < F) return IFX_ERR_INVALID;
+  if (M < 0 || F < 0 || ldgu < 2 * F || (ldq != IFX_LD_TILED && ldq < F)) return IFX_ERR_INVALID;
   if (act != IFX_ACT_GELU_TANH && act != IFX_ACT_SILU) return IFX_ERR_INVALID;
   if (M > 0 && (!gu || !q || !scale)) return IFX_ERR_INVALID;
   const bool vec_ok = aligned16(gu) && ldgu % 8 == 0 && F % 8 == 0 &&
@@ -652,7 +655,8 @@ int ifx_gated_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, cons
 int ifx_moe_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const float* row, const float* col,
                       const float* route_w, int64_t E, int64_t group, int64_t n_routed, void* q, int64_t ldq,
                       float* scale, void* stream) {
-  if (M < 0 || F < 0 || ldgu < 2 * F || ldq < F || E <= 0 || group <= 0 || n_routed < 0) return IFX_ERR_INVALID;
+  if (M < 0 || F < 0 || ldgu < 2 * F || (ldq != IFX_LD_TILED && ldq < F) || E <= 0 || group <= 0 || n_routed < 0)
+    return IFX_ERR_INVALID;
   if (M > 0 && (!gu || !q || !scale || (n_routed > 0 && !route_w))) return IFX_ERR_INVALID;
   if (n_routed == 0)  // no routed columns: the plain SwiGLU
     return ifx_gated_act_quant(gu, ldgu, M, F, row, col, IFX_ACT_SILU, q, ldq, scale, stream);

@@ -11,10 +11,10 @@
 // functions, not the hardware approximations, since angles reach thousands of
 // radians. kv_base may be a device int32 (graph-captured decode steps).
 //
-// Layout: one 4-wave workgroup per token, waves looping over its heads; lane l
-// holds the pairs (i, i + HD/2) for i = l, l + 64 (HD <= 256), and the rotary
-// cos/sin of its i are computed once per wave. Row loads/stores are
-// lane-consecutive elements.
+// Layout: one 4-wave workgroup per (token, group of 4 heads), one head per
+// wave; lane l holds the pairs (i, i + HD/2) for i = l, l + 64 (HD <= 256).
+// A wave issues all loads of its head before the arithmetic. Row loads/stores
+// are lane-consecutive elements.
 
 #include "ifx_abi.h"
 #include "ifx_device.h"
@@ -103,9 +103,9 @@ __device__ __forceinline__ void store8(int out_dtype, void* base, int64_t idx, c
   }
 }
 
-// One workgroup per token; wave w handles heads w, w + 4, ... Each lane holds
-// the pairs (i, i + HD/2) for i = lane + 64 j; the rotary cos/sin of its i are
-// computed once per wave and reused for every head of the token.
+// Workgroup (t, g) handles token t; its wave w handles head 4g + w. Each lane
+// holds the pairs (i, i + HD/2) for i = lane + 64 j and computes the rotary
+// cos/sin of its i.
 template <int NJ>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_split_kernel(QkvArgs a) {
   const int lane = threadIdx.x & 63;
@@ -131,28 +131,59 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_split_kernel(QkvArgs 
     }
   }
 
-  for (int64_t h = wave; h < H; h += kWavesPerBlock) {
-    float lo[NJ], hi[NJ];
+  {
+    // one head per wave: head blockIdx.y * waves + wave
+    const int64_t h = static_cast<int64_t>(blockIdx.y) * kWavesPerBlock + wave;
+    if (h >= H) return;  // wave-uniform; no workgroup barrier follows
+    float lo[NJ], hi[NJ], cl[NJ], ch[NJ], bl[NJ], bh[NJ];
     const int64_t base = t * a.ldqkv + h * a.HD;
+    // all loads of the head first (clamped in-row indices, no per-element branch)
+    if (a.in_f32) {
+      const float* x = static_cast<const float*>(a.qkv) + base;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t i = on[j] ? lane + 64 * j : 0;
+        lo[j] = x[i];
+        hi[j] = x[half + i];
+      }
+    } else {
+      const uint16_t* x = static_cast<const uint16_t*>(a.qkv) + base;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t i = on[j] ? lane + 64 * j : 0;
+        lo[j] = __uint_as_float(static_cast<uint32_t>(x[i]) << 16);
+        hi[j] = __uint_as_float(static_cast<uint32_t>(x[half + i]) << 16);
+      }
+    }
+    if (a.col)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t i = on[j] ? lane + 64 * j : 0;
+        cl[j] = a.col[h * a.HD + i];
+        ch[j] = a.col[h * a.HD + half + i];
+      }
+    if (a.bias)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t i = on[j] ? lane + 64 * j : 0;
+        bl[j] = a.bias[h * a.HD + i];
+        bh[j] = a.bias[h * a.HD + half + i];
+      }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int64_t i = lane + 64 * j;
-      lo[j] = hi[j] = 0.0f;
-      if (!on[j]) continue;
-      lo[j] = load_in(a, base + i);
-      hi[j] = load_in(a, base + half + i);
       if (a.row) {
         lo[j] = lo[j] * r;
         hi[j] = hi[j] * r;
       }
       if (a.col) {
-        lo[j] = lo[j] * a.col[h * a.HD + i];
-        hi[j] = hi[j] * a.col[h * a.HD + half + i];
+        lo[j] = lo[j] * cl[j];
+        hi[j] = hi[j] * ch[j];
       }
       if (a.bias) {
-        lo[j] = lo[j] + a.bias[h * a.HD + i];
-        hi[j] = hi[j] + a.bias[h * a.HD + half + i];
+        lo[j] = lo[j] + bl[j];
+        hi[j] = hi[j] + bh[j];
       }
+      if (!on[j]) lo[j] = hi[j] = 0.0f;
     }
     if (h < a.HQ + a.HKV) {  // wave-uniform
       if (a.qnw) {  // q_norm and k_norm come together
@@ -354,13 +385,15 @@ int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* ro
   QkvArgs a{qkv,  ldqkv, row, col,  bias, q_norm, k_norm, eps,  inv_freq,    pos, ldpos, sections,
             q_out, sq_t, sq_h, k_out, sk_t, sk_h,   v_out,  sv_t, sv_h,        kv_base, kv_base_dev,
             T,    HQ,    HKV, HD,   qkv_dtype == IFX_DTYPE_F32 ? 1 : 0,         out_dtype};
-  const int64_t blocks = T;  // one workgroup per token
-  if (blocks > 0x7FFFFFFFLL) return IFX_ERR_UNSUPPORTED;
+  // one workgroup per (token, group of kWavesPerBlock heads), one head per wave
+  const int64_t hb = (HQ + 2 * HKV + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (T > 0x7FFFFFFFLL || hb > 65535) return IFX_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(hb));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (HD / 2 <= 64)
-    hipLaunchKernelGGL(qkv_split_kernel<1>, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL(qkv_split_kernel<1>, grid, dim3(64 * kWavesPerBlock), 0, st, a);
   else
-    hipLaunchKernelGGL(qkv_split_kernel<2>, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL(qkv_split_kernel<2>, grid, dim3(64 * kWavesPerBlock), 0, st, a);
   return launch_status();
 }
 

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .fp8 import E4M3, _ptr, _rows, _stream, _vec
+from .fp8 import E4M3, _ptr, _qout, _rows, _stream, _vec
 
 GELU_TANH = _lib.ACT_GELU_TANH
 SILU = _lib.ACT_SILU
@@ -32,11 +32,11 @@ def gated_act_quant(gu, q, q_scale, *, row=None, col=None, act=GELU_TANH, num_wa
         raise ValueError("gated_act_quant supports hidden widths up to 16384")
     if act not in (GELU_TANH, SILU):
         raise ValueError(f"act must be GELU_TANH ({GELU_TANH}) or SILU ({SILU})")
-    _, _, ldq = _rows("q", q, E4M3, gu.device, cols=F)
+    qp, ldq = _qout("q", q, M, F, gu.device)
     _vec("q_scale", q_scale, M, device=gu.device)
     _vec("row", row, M, device=gu.device)
     _vec("col", col, F2, device=gu.device)
-    _lib.check(_lib.load().ifx_gated_act_quant(_ptr(gu), ldgu, M, F, _ptr(row), _ptr(col), act, _ptr(q), ldq,
+    _lib.check(_lib.load().ifx_gated_act_quant(_ptr(gu), ldgu, M, F, _ptr(row), _ptr(col), act, qp, ldq,
                                                _ptr(q_scale), _stream(gu.device)), "ifx_gated_act_quant")
 
 
@@ -86,10 +86,10 @@ def moe_act_quant(gu, q, q_scale, route_w, *, row, col, experts, group, n_routed
     E, G, NR = int(experts), int(group), int(n_routed)
     if E <= 0 or G <= 0 or not 0 <= NR <= F:
         raise ValueError("experts and group must be positive and n_routed in [0, F]")
-    _, _, ldq = _rows("q", q, E4M3, dev, cols=F)
+    qp, ldq = _qout("q", q, M, F, dev)
     _vec("q_scale", q_scale, M, device=dev)
     _vec("row", row, M, device=dev)
     _vec("col", col, F2, device=dev)
     _f32_matrix("route_w", route_w, M, E, dev)
     _lib.check(_lib.load().ifx_moe_act_quant(_ptr(gu), ldgu, M, F, _ptr(row), _ptr(col), _ptr(route_w), E, G, NR,
-                                             _ptr(q), ldq, _ptr(q_scale), _stream(dev)), "ifx_moe_act_quant")
+                                             qp, ldq, _ptr(q_scale), _stream(dev)), "ifx_moe_act_quant")

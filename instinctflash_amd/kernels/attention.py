@@ -18,7 +18,7 @@ import ctypes
 import torch
 
 from .. import _lib
-from .fp8 import E4M3, _on_device, _ptr, _rows, _stream, _vec
+from .fp8 import _on_device, _ptr, _qout, _stream, _vec
 
 _DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 
@@ -121,13 +121,11 @@ def attention(q, k, v, out=None, *, scale=None, kv_len=None, kv_extra=None, max_
             raise ValueError("the fused FP8 output needs a split workspace")
         if B != 1:
             raise ValueError("fused FP8 output supports batch 1")
-        _, _, ldq8 = _rows("q8", q8, E4M3, dev, cols=Hq * D)
-        if q8.shape[0] != Tq:
-            raise ValueError(f"q8 must have {Tq} rows")
+        q8p, ldq8 = _qout("q8", q8, Tq, Hq * D, dev)
         _vec("q8_scale", q8_scale, Tq, device=dev)
     _lib.check(_lib.load().ifx_attention(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _DT[q.dtype], B, Tq, Hq, Tk, Hkv, D, qs, ks, vs, os_, static_len,
         _ptr(kv_len) if dynamic else None, _ptr(kv_extra), 1 if causal else 0, int(causal_offset), _ptr(kv_index),
-        kv_index.numel() if kv_index is not None else 0, float(scale), splits, _ptr(ws), ws_bytes, _ptr(q8), ldq8,
+        kv_index.numel() if kv_index is not None else 0, float(scale), splits, _ptr(ws), ws_bytes, q8p if q8 is not None else None, ldq8,
         _ptr(q8_scale), _stream(dev)), "ifx_attention")
     return out

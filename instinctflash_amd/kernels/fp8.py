@@ -112,6 +112,21 @@ def _vec(name, t, n, dtype=torch.float32, device=None):
     return t
 
 
+def _qout(name, q, M, K, device):
+    """E4M3 output operand [M, K]: a row-strided tensor, or a :class:`TiledRows`
+    (the skinny tile layout, M <= 64). Returns (pointer, row stride) with the
+    row stride IFX_LD_TILED (0) for the tile layout."""
+    if isinstance(q, TiledRows):
+        if (q.M, q.K) != (M, K) or q.q.dtype != E4M3 or q.device != device or \
+                q.q.numel() != _lib.load().ifx_quant_rows_tiled_bytes(M, K):
+            raise ValueError(f"{name} does not hold the tile layout of a [{M}, {K}] operand")
+        return q.q.data_ptr(), _lib.LD_TILED
+    rows, _, ld = _rows(name, q, E4M3, device, cols=K)
+    if rows != M:
+        raise ValueError(f"{name} must have {M} rows")
+    return q.data_ptr(), ld
+
+
 _WORKSPACES: dict = {}
 
 

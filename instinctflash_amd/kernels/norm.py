@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .fp8 import E4M3, _ptr, _rows, _stream, _vec
+from .fp8 import E4M3, _ptr, _qout, _rows, _stream, _vec
 
 
 def row_quant(x, q, q_scale, *, row=None, col=None, bias=None, gelu=False, num_warps=None):
@@ -23,14 +23,14 @@ def row_quant(x, q, q_scale, *, row=None, col=None, bias=None, gelu=False, num_w
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("row_quant expects bf16 or fp16 input")
     M, D, ldx = _rows("x", x, x.dtype)
-    _, _, ldq = _rows("q", q, E4M3, x.device, cols=D)
+    qp, ldq = _qout("q", q, M, D, x.device)
     _vec("q_scale", q_scale, M, device=x.device)
     _vec("row", row, M, device=x.device)
     _vec("col", col, D, device=x.device)
     _vec("bias", bias, D, device=x.device)
     flags = (_lib.RQ_GELU if gelu else 0) | (_lib.RQ_F16 if x.dtype == torch.float16 else 0)
     _lib.check(_lib.load().ifx_row_quant(_ptr(x), ldx, M, D, _ptr(row), _ptr(col), _ptr(bias),
-                                         flags, _ptr(q), ldq, _ptr(q_scale),
+                                         flags, qp, ldq, _ptr(q_scale),
                                          _stream(x.device)), "ifx_row_quant")
 
 
@@ -108,11 +108,11 @@ def residual_norm_quant(res, *, delta=None, delta_row=None, delta_col=None, bias
         _table(name, t, D, indexed, dev)
     if (mod_scale is None) != (mod_shift is None):
         raise ValueError("mod_scale and mod_shift come together")
-    ldq = 0
+    qp, ldq = None, 0
     if q is not None:
-        Mq, _, ldq = _rows("q", q, E4M3, dev, cols=D)
-        if Mq != M or q_scale is None:
-            raise ValueError("q needs M rows and a q_scale vector")
+        if q_scale is None:
+            raise ValueError("q needs a q_scale vector")
+        qp, ldq = _qout("q", q, M, D, dev)
         _vec("q_scale", q_scale, M, device=dev)
     ldy = 0
     if y is not None:
@@ -139,5 +139,5 @@ def residual_norm_quant(res, *, delta=None, delta_row=None, delta_col=None, bias
     _lib.check(_lib.load().ifx_residual_norm_quant(
         _ptr(res), dt(res), ldres, _ptr(delta), dt(delta), lddelta, _ptr(delta_row), _ptr(delta_col), _ptr(bias),
         _ptr(gate), _ptr(weight), _ptr(beta), _ptr(mod_scale), _ptr(mod_shift), _ptr(mod_index), flags, float(eps),
-        _ptr(q), ldq, _ptr(q_scale), _ptr(y), dt(y), ldy, _ptr(rw), _ptr(rb), _ptr(ro), rE, int(rK), float(rS), M, D,
+        qp, ldq, _ptr(q_scale), _ptr(y), dt(y), ldy, _ptr(rw), _ptr(rb), _ptr(ro), rE, int(rK), float(rS), M, D,
         _stream(dev)), "ifx_residual_norm_quant")

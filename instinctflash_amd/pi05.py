@@ -11,9 +11,17 @@ Weights are per-output-channel FP8 (``quantize_weight``); the whole loop is
 graph-capturable (the prefix length lives in device memory).
 
 It exists to run the drop-in kernels end to end at the engine's real shapes:
-``Pi05Expert.random`` builds random weights of the published architecture
+``random_weights`` builds random weights of the published architecture
 (Gemma-300M expert: width 1024, MLP 4096, 18 layers, 8 query heads and one KV
 head of 256), since no checkpoint is available here.
+
+``reference_calls=True`` makes exactly the reference's calls (row-major FP8
+operands, attention into fp16 then ``row_quant``). The default keeps the same
+math but lays the loop out for gfx950: weights in the skinny tile layout
+(``pack_skinny``), every FP8 activation written by its producer in the tile
+layout the M <= 64 GEMM reads with 1 KB loads, and the attention's split-KV
+combine emitting the output projection's FP8 operand directly (one kernel per
+layer fewer).
 """
 from __future__ import annotations
 
@@ -21,8 +29,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels import E4M3, Fp8Weight, attention, gated_act_quant, gemm, qkv_split, quantize_weight, \
-    residual_norm_quant, rope_inv_freq, row_quant
+from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, pack_skinny, \
+    qkv_split, quantize_weight, residual_norm_quant, rope_inv_freq, row_quant
 from .kernels.activation import GELU_TANH
 
 EX_D, EX_FF = 1024, 4096
@@ -83,8 +91,9 @@ class Pi05Expert:
     returns the chunk's actions x_t [chunk, 32] (reference engine.py:212-245).
     """
 
-    def __init__(self, weights: ExpertWeights, device, *, smax=1024, chunk=50):
+    def __init__(self, weights: ExpertWeights, device, *, smax=1024, chunk=50, reference_calls=False):
         self.w = weights
+        self.reference_calls = bool(reference_calls)
         self.dev = torch.device(device)
         self.chunk = int(chunk)
         self.smax = int(smax)
@@ -110,6 +119,16 @@ class Pi05Expert:
         self.out_w_dt = (weights.action_out_w * dt).t().contiguous()
         self.out_b_dt = (weights.action_out_b * dt).contiguous()
         self.in_w_t = weights.action_in_w.t().contiguous()
+        if not self.reference_calls:
+            from . import _lib
+            lib = _lib.load()
+            tiled = lambda k: TiledRows(torch.zeros(lib.ifx_quant_rows_tiled_bytes(A, k), dtype=E4M3,  # noqa: E731
+                                                    device=dev), A, k)
+            self.xq, self.oq, self.hq = tiled(EX_D), tiled(HEADS * HEAD_DIM), tiled(EX_FF)
+            self.layers = [ExpertLayer(pack_skinny(L.qkv), pack_skinny(L.o), pack_skinny(L.gate_up),
+                                       pack_skinny(L.down)) for L in weights.layers]
+            splits = max(2, min(16, -(-(self.smax + A) // 128)))
+            self.split = SplitWorkspace(1, A, HEADS, 1, HEAD_DIM, splits, dev)
 
     def q8v(self, rows, cols):
         return self.q8[: rows * cols].view(rows, cols)
@@ -126,7 +145,10 @@ class Pi05Expert:
         torch.arange(n, n + self.chunk, out=self.pos_chunk[:, 0])
 
     def forward(self, noise=None):
-        """Reference engine.py:212-245 (`_expert`), call for call."""
+        """Reference engine.py:212-245 (`_expert`); call for call with
+        ``reference_calls``, else the tile-layout form of the same math."""
+        if not self.reference_calls:
+            return self._forward_tiled(noise)
         w, A = self.w, self.chunk
         q8, raw, s = self.q8v, self.rawv, self.scale
         if noise is not None:
@@ -159,6 +181,43 @@ class Pi05Expert:
                     residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
                                         gate=mf[i, 2], mod_scale=ma[i + 1, 0], mod_shift=ma[i + 1, 1],
                                         q=q8(A, EX_D), q_scale=s[0])
+                else:
+                    mfin = w.mod_final[step]
+                    residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
+                                        gate=mf[i, 2], mod_scale=mfin[0], mod_shift=mfin[1], y=self.dy)
+            self.x_t.addmm_(self.dy, self.out_w_dt).add_(self.out_b_dt)
+        return self.x_t
+
+    def _forward_tiled(self, noise=None):
+        w, A = self.w, self.chunk
+        raw, s = self.rawv, self.scale
+        xq, oq, hq = self.xq, self.oq, self.hq
+        if noise is not None:
+            self.noise.copy_(noise)
+        self.x_t.copy_(self.noise)
+        qv = self.q16[:A].view(1, A, HEADS, HEAD_DIM)
+        last = len(self.layers) - 1
+        for step in range(w.steps):
+            torch.addmm(w.action_in_b, self.x_t, self.in_w_t, out=self.dx)
+            ma, mf = w.mod_attn[step], w.mod_ffn[step]
+            residual_norm_quant(self.dx, mod_scale=ma[0, 0], mod_shift=ma[0, 1], q=xq, q_scale=s[0])
+            for i, L in enumerate(self.layers):
+                gemm(xq, L.qkv, raw(A, QKV_N))
+                qkv_split(raw(A, QKV_N), self.q16[:A], self.kc[i], self.vc[i], heads_q=HEADS, heads_kv=1,
+                          head_dim=HEAD_DIM, inv_freq=self.inv_freq, pos=self.pos_chunk, row=s[0],
+                          col=L.qkv.scale, kv_base=self.prefix_len)
+                attention(qv, self.kc[i][None], self.vc[i][None], kv_len=self.kv_len, scale=HEAD_DIM ** -0.5,
+                          split=self.split, q8=oq, q8_scale=s[1])
+                gemm(oq, L.o, raw(A, EX_D))
+                residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.o.scale,
+                                    gate=ma[i, 2], mod_scale=mf[i, 0], mod_shift=mf[i, 1], q=xq, q_scale=s[0])
+                gemm(xq, L.gate_up, raw(A, 2 * EX_FF))
+                gated_act_quant(raw(A, 2 * EX_FF), hq, s[1], row=s[0], col=L.gate_up.scale, act=GELU_TANH)
+                gemm(hq, L.down, raw(A, EX_D))
+                if i < last:
+                    residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
+                                        gate=mf[i, 2], mod_scale=ma[i + 1, 0], mod_shift=ma[i + 1, 1],
+                                        q=xq, q_scale=s[0])
                 else:
                     mfin = w.mod_final[step]
                     residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,

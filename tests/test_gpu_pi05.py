@@ -5,7 +5,8 @@ Checks: (1) against a plain PyTorch fp32 restatement of the same layer math
 (dequantized FP8 weights, unquantized activations, fp32 attention and RoPE) --
 the FP8 activation rounding of every projection input makes this a tolerance
 check: cosine >= 0.999 on the residual stream and the actions after 2 layers x
-2 steps; (2) a captured graph replays the eager result bit for bit and follows
+2 steps -- for the reference's call sequence and for the tile-layout form, and
+the two forms agree to the same bar; (2) a captured graph replays the eager result bit for bit and follows
 the device prefix length; (3) the real shapes (18 layers, 10 steps, an
 800-row prefix) run under a graph with finite outputs.
 """
@@ -71,10 +72,10 @@ def _reference(eng, noise, prefix):
     return x_t, dx
 
 
-def _engine(gpu, layers, steps, prefix, smax, seed=0):
+def _engine(gpu, layers, steps, prefix, smax, seed=0, reference_calls=False):
     from instinctflash_amd.pi05 import Pi05Expert, random_weights
     w = random_weights(gpu, layers=layers, steps=steps, seed=seed)
-    eng = Pi05Expert(w, gpu, smax=smax)
+    eng = Pi05Expert(w, gpu, smax=smax, reference_calls=reference_calls)
     g = torch.Generator().manual_seed(seed + 1)
     eng.kc[:, :prefix] = torch.randn(layers, prefix, 1, 256, generator=g).half().to(gpu)
     eng.vc[:, :prefix] = torch.randn(layers, prefix, 1, 256, generator=g).half().to(gpu)
@@ -88,14 +89,24 @@ def _cos(a, b):
     return float(a @ b / (a.norm() * b.norm()))
 
 
-def test_matches_fp32_restatement(gpu):
-    eng, noise = _engine(gpu, layers=2, steps=2, prefix=300, smax=512)
+@pytest.mark.parametrize("reference_calls", [True, False])
+def test_matches_fp32_restatement(gpu, reference_calls):
+    eng, noise = _engine(gpu, layers=2, steps=2, prefix=300, smax=512, reference_calls=reference_calls)
     ref_x, ref_dx = _reference(eng, noise, 300)
     x = eng.forward(noise).clone()
     torch.cuda.synchronize()
     assert torch.isfinite(x).all()
     assert _cos(eng.dx, ref_dx) > 0.999, _cos(eng.dx, ref_dx)
     assert _cos(x, ref_x) > 0.999, _cos(x, ref_x)
+
+
+def test_forms_agree(gpu):
+    ref_eng, noise = _engine(gpu, layers=2, steps=2, prefix=300, smax=512, seed=9, reference_calls=True)
+    eng, _ = _engine(gpu, layers=2, steps=2, prefix=300, smax=512, seed=9)
+    a = ref_eng.forward(noise).clone()
+    b = eng.forward(noise).clone()
+    torch.cuda.synchronize()
+    assert _cos(a, b) > 0.9999 and _cos(ref_eng.dx, eng.dx) > 0.9999
 
 
 def test_graph_replay_and_prefix_length(gpu):
