@@ -41,16 +41,24 @@ class SplitWorkspace:
 _AUTO_SPLIT: dict = {}
 
 
+def split_count(B, Tq, Hq, Hkv, Tk) -> int:
+    """Key ranges for a launch with few query-row blocks (workgroups of 128 query
+    rows): about 256 workgroups in total, at least 64 keys per range, 2..16
+    ranges (measured on MI355X: the 51-token pi05 chunk over 882 keys runs best
+    at 14, the 800-token prefix at 4-6). 1 when the row blocks alone fill the GPU."""
+    blocks = -(-(Tq * (Hq // Hkv)) // 128) * Hkv * B
+    if blocks >= 128 or Tk < 128:
+        return 1
+    return int(max(2, min(16, -(-Tk // 64), round(256 / blocks))))
+
+
 def _auto_split(B, Tq, Hq, Hkv, D, Tk, device):
     """Split workspace for launches with too few row blocks to fill the GPU
-    (fewer than 128 workgroups of 128 query rows): the keys are cut into ranges
-    of about 128 (2..16 ranges), so each workgroup's chain of dependent key
-    blocks stays short. Allocated once per geometry and device, then reused
-    (calls on one device are stream-ordered by the caller)."""
-    blocks = -(-(Tq * (Hq // Hkv)) // 128) * Hkv * B
-    if blocks >= 128 or Tk < 256 or Hq * 16 > 1024:
+    (:func:`split_count`), allocated once per geometry and device and then
+    reused (calls on one device are stream-ordered by the caller)."""
+    splits = split_count(B, Tq, Hq, Hkv, Tk)
+    if splits < 2 or Hq * splits > 1024:
         return None
-    splits = int(min(16, max(2, -(-Tk // 128))))
     key = (device, B, Tq, Hq, Hkv, D, splits)
     ws = _AUTO_SPLIT.get(key)
     if ws is None:

@@ -32,6 +32,7 @@ import torch
 from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, pack_skinny, \
     qkv_split, quantize_weight, residual_norm_quant, rope_inv_freq, row_quant
 from .kernels.activation import GELU_TANH
+from .kernels.attention import split_count
 
 EX_D, EX_FF = 1024, 4096
 HEADS, HEAD_DIM = 8, 256
@@ -127,7 +128,7 @@ class Pi05Expert:
             self.xq, self.oq, self.hq = tiled(EX_D), tiled(HEADS * HEAD_DIM), tiled(EX_FF)
             self.layers = [ExpertLayer(pack_skinny(L.qkv), pack_skinny(L.o), pack_skinny(L.gate_up),
                                        pack_skinny(L.down)) for L in weights.layers]
-            splits = max(2, min(16, -(-(self.smax + A) // 128)))
+            splits = max(2, split_count(1, A, HEADS, 1, self.smax + A))
             self.split = SplitWorkspace(1, A, HEADS, 1, HEAD_DIM, splits, dev)
 
     def q8v(self, rows, cols):

@@ -541,13 +541,16 @@ class MoeAct:
 class Attn:
     """``attention`` at the pi05 shapes (8 query heads, 1 KV head of 256 dims):
     the 51-token action chunk over an 800-token prefix plus itself, split over
-    8 key ranges with the fused per-token E4M3 output row (the o-projection's A
-    operand), or the 800-token prefix self-attention. Work: 4 * Tq * Hq * Tk * D
+    key ranges (``split_count``) with the fused per-token E4M3 output row (the
+    o-projection's A operand), or the 800-token prefix self-attention (keys
+    split automatically). Work: 4 * Tq * Hq * Tk * D
     FLOP (bf16 matrix cores); algorithmic bytes: q, k, v read once, the output
     (bf16 row, or e4m3 row + scale) written once."""
 
-    def __init__(self, dev, Tq=51, Tk=851, Hq=8, Hkv=1, D=256, splits=8, q8=True, seed=0):
-        from .kernels.attention import SplitWorkspace, attention
+    def __init__(self, dev, Tq=51, Tk=851, Hq=8, Hkv=1, D=256, splits=None, q8=True, seed=0):
+        from .kernels.attention import SplitWorkspace, attention, split_count
+        if splits is None:
+            splits = max(2, split_count(1, Tq, Hq, Hkv, Tk)) if q8 else 1
         self.attention, self.Tq, self.Tk, self.Hq, self.Hkv, self.D = attention, Tq, Tk, Hq, Hkv, D
         g = _gen(seed)
         self.q = torch.randn(1, Tq, Hq, D, generator=g).to(torch.bfloat16).to(dev)
