@@ -36,6 +36,7 @@
 //    by the last workgroup to arrive (deterministic, no waiting).
 
 #include <algorithm>
+#include <type_traits>
 
 #include "ifx_abi.h"
 #include "ifx_device.h"
@@ -79,15 +80,22 @@ __device__ __forceinline__ float4 epi_sw4(const Epi& e, int64_t n) {
   return load_f4_or(e.sw, n, 1.0f);
 }
 
+// y * g rounded on its own: the residual add that follows must not fuse with
+// it, so every epilogue rounds the adaLN-gated value identically.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 // y (four consecutive output columns c..c+3 of row m, after activation) ->
 // gate, residual, store.
 __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, float* y) {
   if (e.flags & IFX_EPI_GATE) {
     const uint2 g = *reinterpret_cast<const uint2*>(e.gate + c);
-    y[0] *= __uint_as_float(g.x << 16);
-    y[1] *= __uint_as_float(g.x & 0xFFFF0000u);
-    y[2] *= __uint_as_float(g.y << 16);
-    y[3] *= __uint_as_float(g.y & 0xFFFF0000u);
+    y[0] = mul_rn(y[0], __uint_as_float(g.x << 16));
+    y[1] = mul_rn(y[1], __uint_as_float(g.x & 0xFFFF0000u));
+    y[2] = mul_rn(y[2], __uint_as_float(g.y << 16));
+    y[3] = mul_rn(y[3], __uint_as_float(g.y & 0xFFFF0000u));
   }
   if (e.flags & IFX_EPI_RESIDUAL) {
     if (e.flags & IFX_EPI_RES_F32) {
@@ -707,6 +715,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   //     scales, bias and adaLN gate are loaded once, the tile's token scales
   //     are staged in LDS, and a fragment row's residual loads are all issued
   //     before its math. Every output row is written as one contiguous segment.
+  // The epilogue flags are resolved once per workgroup into a compile-time
+  // mode (activation, gate, residual; bf16 residual and output), so the row
+  // loop carries no per-element branches; other flag sets take the
+  // runtime-flag loop.
   // The barrier keeps the stage buffers alive until every wave is done with
   // its MFMAs and publishes the token scales.
   constexpr int kCols = GLU ? 16 * kFN : 32 * kFN;  // output columns of a wave tile
@@ -737,61 +749,125 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   const float gta[4] = {__uint_as_float(g2.x << 16), __uint_as_float(g2.x & 0xFFFF0000u),
                         __uint_as_float(g2.y << 16), __uint_as_float(g2.y & 0xFFFF0000u)};
   float* tile = reinterpret_cast<float*>(smem) + wave * 32 * kPitch;
-  const bool swiglu = (e.flags & IFX_EPI_SWIGLU) != 0;
-  const bool gelu = (e.flags & IFX_EPI_GELU_TANH) != 0;
-  const bool has_gate = (e.flags & IFX_EPI_GATE) != 0;
-  const bool has_res = (e.flags & IFX_EPI_RESIDUAL) != 0;
   const int r0 = lane / kLanesPerRow;
 
+  // Mode bits: 1 GELU-tanh (GeGLU for GLU), 2 SiLU (SwiGLU), 4 gate,
+  // 8 residual, 16 runtime flags (f32 residual or output, any combination).
+  auto rows = [&](auto mode_tag) {
+    constexpr int MD = decltype(mode_tag)::value;
+    constexpr bool kRt = (MD & 16) != 0;
+    const int fl = e.flags;
+    const bool act_gelu = kRt ? (fl & (GLU ? IFX_EPI_GEGLU : IFX_EPI_GELU_TANH)) != 0 : (MD & 1) != 0;
+    const bool act_silu = kRt ? (fl & IFX_EPI_SWIGLU) != 0 : (MD & 2) != 0;
+    const bool has_gate = kRt ? (fl & IFX_EPI_GATE) != 0 : (MD & 4) != 0;
+    const bool has_res = kRt ? (fl & IFX_EPI_RESIDUAL) != 0 : (MD & 8) != 0;
 #pragma unroll
-  for (int j = 0; j < kFM; ++j) {
+    for (int j = 0; j < kFM; ++j) {
 #pragma unroll
-    for (int i = 0; i < kFN; ++i)
+      for (int i = 0; i < kFN; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    float4 res[kRowIters];
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const int64_t mrow = mw + j * 32 + r0;         // token of pass 0
+      const int64_t left = e.M - (mw + j * 32);      // rows of this fragment row inside M
+      // residual rows are loaded kResBatch at a time, ahead of their math
+      constexpr int kResBatch = kRowIters < 8 ? kRowIters : 8;
+      if (col_ok) {
+        uint16_t* orow = static_cast<uint16_t*>(e.out) + mrow * e.ldo + c_out;
 #pragma unroll
-    for (int t = 0; t < kRowIters; ++t) {
-      const int64_t m = mw + j * 32 + r0 + t * kRowsPerPass;
-      res[t] = (col_ok && has_res && m < e.M) ? load_res4(e, m, c_out) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+        for (int t0 = 0; t0 < kRowIters; t0 += kResBatch) {
+        float4 res[kResBatch];
 #pragma unroll
-    for (int t = 0; t < kRowIters; ++t) {
-      const int r = r0 + t * kRowsPerPass;
-      const int64_t m = mw + j * 32 + r;
-      if (col_ok && m < e.M) {
-        const float sa = s_sa[wm * kWT + j * 32 + r];
-        const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
-        const float va[4] = {v.x, v.y, v.z, v.w};
-        const float ra[4] = {res[t].x, res[t].y, res[t].z, res[t].w};
-        float y[4];
-        if constexpr (GLU) {
-          const float4 w = *reinterpret_cast<const float4*>(tile + r * kPitch + pc + 16);
-          const float wa[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float gv = va[u] * sa * swa[u] + ba[u];
-            const float uv = wa[u] * sa * swu[u] + bu[u];
-            y[u] = (swiglu ? silu(gv) : gelu_tanh(gv)) * uv;
-          }
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            y[u] = va[u] * sa * swa[u] + ba[u];
-            if (gelu) y[u] = gelu_tanh(y[u]);
+        for (int tb = 0; tb < kResBatch; ++tb) {
+          const int t = t0 + tb;
+          const int r = r0 + t * kRowsPerPass;
+          if constexpr (kRt) {
+            res[tb] = (has_res && r < left) ? load_res4(e, mrow + t * kRowsPerPass, c_out)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+          } else if constexpr ((MD & 8) != 0) {
+            const uint16_t* rp = static_cast<const uint16_t*>(e.res) + c_out;
+            const int64_t m = min(mrow + t * kRowsPerPass, e.M - 1);
+            const uint2 rv = *reinterpret_cast<const uint2*>(rp + m * e.ldr);
+            res[tb] = make_float4(__uint_as_float(rv.x << 16), __uint_as_float(rv.x & 0xFFFF0000u),
+                                 __uint_as_float(rv.y << 16), __uint_as_float(rv.y & 0xFFFF0000u));
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (has_gate) y[u] = y[u] * gta[u];
-          if (has_res) y[u] = ra[u] + y[u];
+        for (int tb = 0; tb < kResBatch; ++tb) {
+          const int t = t0 + tb;
+          const int r = r0 + t * kRowsPerPass;
+          if (r < left) {
+            const float sa = s_sa[wm * kWT + j * 32 + r];
+            const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
+            const float va[4] = {v.x, v.y, v.z, v.w};
+            float y[4];
+            if constexpr (GLU) {
+              const float4 w = *reinterpret_cast<const float4*>(tile + r * kPitch + pc + 16);
+              const float wa[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const float gv = va[u] * sa * swa[u] + ba[u];
+                const float uv = wa[u] * sa * swu[u] + bu[u];
+                y[u] = (act_silu ? silu(gv) : gelu_tanh(gv)) * uv;
+              }
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                y[u] = va[u] * sa * swa[u] + ba[u];
+                if (act_gelu) y[u] = gelu_tanh(y[u]);
+              }
+            }
+            if (has_gate) {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) y[u] = mul_rn(y[u], gta[u]);
+            }
+            if (has_res) {
+              y[0] = res[tb].x + y[0];
+              y[1] = res[tb].y + y[1];
+              y[2] = res[tb].z + y[2];
+              y[3] = res[tb].w + y[3];
+            }
+#ifdef IFX_DBG_NO_STORE
+            if (y[0] == 1234.5f && y[1] == -1.f)
+#endif
+            {
+              if constexpr (kRt) {
+                epi_store4(e, mrow + t * kRowsPerPass, c_out, y);
+              } else {
+                uint2 o;
+                o.x = pack_bf16x2(y[0], y[1]);
+                o.y = pack_bf16x2(y[2], y[3]);
+                *reinterpret_cast<uint2*>(orow + static_cast<int64_t>(t * kRowsPerPass) * e.ldo) = o;
+              }
+            }
+          }
         }
-        epi_store4(e, m, c_out, y);
+        }
       }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  const int fl = e.flags;
+  const bool plain_io = !(fl & (IFX_EPI_OUT_F32 | IFX_EPI_RES_F32));
+  const int gr = ((fl & IFX_EPI_GATE) ? 4 : 0) | ((fl & IFX_EPI_RESIDUAL) ? 8 : 0);
+  using std::integral_constant;
+  if constexpr (GLU) {
+    if (plain_io && gr == 0) {
+      if (fl & IFX_EPI_SWIGLU) rows(integral_constant<int, 2>{});
+      else rows(integral_constant<int, 1>{});
+    } else {
+      rows(integral_constant<int, 16>{});
+    }
+  } else {
+    const bool gl = (fl & IFX_EPI_GELU_TANH) != 0;
+    if (!plain_io) rows(integral_constant<int, 16>{});
+    else if (gl && gr == 0) rows(integral_constant<int, 1>{});
+    else if (gl) rows(integral_constant<int, 16>{});
+    else if (gr == 0) rows(integral_constant<int, 0>{});
+    else if (gr == 8) rows(integral_constant<int, 8>{});
+    else if (gr == 12) rows(integral_constant<int, 12>{});
+    else rows(integral_constant<int, 16>{});
   }
 }
 
@@ -1082,7 +1158,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (e.flags & IFX_EPI_GATE) y[r] = y[r] * gate_epi[r];
+      if (e.flags & IFX_EPI_GATE) y[r] = mul_rn(y[r], gate_epi[r]);
       if (e.flags & IFX_EPI_RESIDUAL) y[r] = res_epi[r] + y[r];
     }
     epi_store4(e, m_epi, c_epi, y);
