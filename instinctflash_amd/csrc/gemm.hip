@@ -488,7 +488,7 @@ __device__ __forceinline__ v4f quad(const v16f& v, int q) {
   return v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
 }
 
-template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM, bool PIPE>
+template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM>
 __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __restrict__ A, int64_t lda,
                                                      const uint8_t* __restrict__ W, int64_t ldw, int64_t K,
                                                      TileMap tmap, Epi e, Partials part) {
@@ -582,71 +582,6 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
   };
 
-  if constexpr (PIPE) {
-    // Register-pipelined loop (KB = 64: one MFMA K step per stage). The
-    // fragments of stage kt+1 are read into the second register set right after
-    // the barrier that publishes stage kt+1, then the MFMAs of stage kt run on
-    // the first set, so LDS latency hides under matrix-core work even with one
-    // wave per SIMD. The DMA issued at iteration kt refills the slot of stage
-    // kt-1, whose fragments every wave consumed during iteration kt-1.
-    static_assert(KB == 64 && STAGES >= 3, "pipelined loop: 64-byte stages, >= 3-deep ring");
-    auto wait_stages = [&](int n) {  // at most n stages of this wave's DMA still in flight
-      if (n <= 0) wait_vmcnt<0>();
-      else if (n == 1) wait_vmcnt<kLoads>();
-      else if (n == 2) wait_vmcnt<2 * kLoads>();
-      else wait_vmcnt<3 * kLoads>();
-    };
-    const int c0 = 2 * fhalf;
-    auto load_frags = [&](const uint8_t* base, v8i (&wf)[kFN], v8i (&af)[kFM]) {
-#pragma unroll
-      for (int j = 0; j < kFM; ++j) {
-        const int row = BN + wm * kWT + j * 32 + frow;
-        af[j] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
-      }
-#pragma unroll
-      for (int i = 0; i < kFN; ++i) {
-        const int row = wn * (32 * kFN) + i * 32 + frow;
-        wf[i] = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
-      }
-    };
-    v8i wa[kFN], aa[kFM], wb[kFN], ab[kFM];  // two fragment register sets
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-      if (s < nk) issue(s);
-    wait_stages(min(STAGES - 2, nk - 1));
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    load_frags(smem, wa, aa);
-    // publish stage t+1, refill the ring, read stage t+1 into the other set
-    auto advance = [&](int t, v8i (&wn_)[kFN], v8i (&an_)[kFM]) {
-      wait_stages(min(t + STAGES - 2, nk - 1) - (t + 1));
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-#ifndef IFX_DBG_NO_DMA
-      if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
-#endif
-      load_frags(smem + ((t + 1) % STAGES) * kStage, wn_, an_);
-    };
-    auto mfmas = [&](const v8i (&wc)[kFN], const v8i (&ac)[kFM]) {
-#ifndef IFX_DBG_NO_MFMA
-#pragma unroll
-      for (int i = 0; i < kFN; ++i)
-#pragma unroll
-        for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wc[i], ac[j], acc[i][j]);
-#endif
-    };
-    // two stages per trip so the register sets alternate statically
-    int kt = 0;
-    for (; kt + 2 <= nk; kt += 2) {
-      if (kt + 1 < nk) advance(kt, wb, ab);
-      mfmas(wa, aa);
-      if (kt + 2 < nk) advance(kt + 1, wa, aa);
-      mfmas(wb, ab);
-    }
-    if (kt < nk) mfmas(wa, aa);  // odd stage count: the last stage is in set a
-  } else {
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nk) issue(s);
@@ -663,7 +598,6 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 #ifndef IFX_DBG_NO_MFMA
     compute(smem + (kt % STAGES) * kStage);
 #endif
-  }
   }
 
 #ifdef IFX_DBG_NO_EPI
@@ -1208,7 +1142,7 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int bn
   return p;
 }
 
-template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM = 2, bool PIPE = false>
+template <int BM, int BN, int KB, int STAGES, int OCC, bool GLU, int FM = 2>
 int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e,
                void* ws, size_t ws_bytes, hipStream_t st) {
   const BigPlan p = big_plan(e.M, e.N, K, BM, BN, KB);
@@ -1219,7 +1153,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
     part.base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);  // tickets stay untouched
   }
   const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
-  hipLaunchKernelGGL((gemm_big<BM, BN, KB, STAGES, OCC, GLU, FM, PIPE>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
+  hipLaunchKernelGGL((gemm_big<BM, BN, KB, STAGES, OCC, GLU, FM>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
                      0, st, a, lda, w, ldw, K, t, e, part);
   if (p.ksplit > 1) {
     const int64_t threads = e.M * ((GLU ? e.N / 2 : e.N) / 4);
