@@ -577,7 +577,13 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         const int row = wn * (32 * kFN) + i * 32 + frow;
         const v8i wf = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
 #pragma unroll
-        for (int j = 0; j < kFM; ++j) acc[i][j] = mfma32(wf, af[j], acc[i][j]);
+        for (int j = 0; j < kFM; ++j) {
+#ifdef IFX_DBG_READS_ONLY
+          acc[i][j][0] += __int_as_float((wf[0] ^ af[j][1]) & 0x3FFFFF) + __int_as_float((wf[7] ^ af[j][6]) & 0x3FFFFF);
+#else
+          acc[i][j] = mfma32(wf, af[j], acc[i][j]);
+#endif
+        }
       }
     }
   };
