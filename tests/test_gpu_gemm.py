@@ -134,6 +134,22 @@ def test_residual_and_gate(gpu, oracle_mod, M, res_dtype):
     assert torch.equal(r, expect), "in-place residual update differs"
 
 
+@pytest.mark.parametrize("act,res,gate", [("gelu_tanh", True, False), ("gelu_tanh", True, True), (None, False, True),
+                                          ("geglu", True, False), ("swiglu", True, True)])
+def test_large_m_epilogue_combinations(gpu, oracle_mod, act, res, gate):
+    # large-M kernel: flag sets outside its compile-time modes (activation with a
+    # residual, gate without residual, GLU with residual) against the oracle, and
+    # the bf16 store equal to the rounded fp32 result of the same call
+    from instinctflash_amd.kernels import pack_glu
+    M, N, K = 2000, 6144, 512  # >= 192 tiles of 256 x 256: no K split, ragged last token tile
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=31, bias=True)
+    n_out = N // 2 if act in ("geglu", "swiglu") else N
+    r = torch.randn((M, n_out), generator=g).to(torch.bfloat16) if res else None
+    gt = torch.rand(n_out, generator=g).to(torch.bfloat16) if gate else None
+    w = pack_glu(fw) if act in ("geglu", "swiglu") else fw
+    _check(gpu, oracle_mod, qa, sa, w, f"{act} res={res} gate={gate}", ref_w=fw, act=act, residual=r, gate=gt)
+
+
 def test_fp32_output(gpu, oracle_mod):
     qa, sa, fw, _ = _make(gpu, 100, 512, 512, seed=8, bias=True)
     o32, _ = _check(gpu, oracle_mod, qa, sa, fw, "f32 out")
