@@ -1138,7 +1138,11 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int bn
   const int64_t nk = K / kb;
   int64_t s = 1;
   if (tiles < 192) {
-    s = (320 + tiles - 1) / tiles;
+    // As many slices as keep the grid within one workgroup per CU: a grid of
+    // 1-2 workgroups per CU leaves the CUs that get two the critical path
+    // (measured: 816x2048x16384 51 vs 57 us at 224 vs 336 workgroups;
+    // 1024x2048x11008 44 vs 51 us at 256 vs 320).
+    s = 256 / tiles;
     if (s > nk / 4) s = nk / 4;
     if (s < 1) s = 1;
   }
