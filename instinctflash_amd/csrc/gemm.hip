@@ -1263,9 +1263,10 @@ inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; 
 //    round) but 512 tiles of 192 rows (two full rounds): 329 -> 302 us for
 //    K = 14336.
 //  * kSmall: fewer than 192 tiles of 256 x 256 and K <= 4096 -- 64 tokens x
-//    128 weight rows, 2 waves, four workgroups per CU, usually no split (e.g.
-//    1024 x 2560 x 2048: 28 -> 18 us against split-K narrow tiles, whose fp32
-//    partials cost more than the short K loop);
+//    128 weight rows, 128-byte stages, 4 waves of 64 x 32 (short MFMA chains
+//    per wave: the loop is latency-bound at these sizes), two workgroups per
+//    CU, usually no split (1024 x 2560 x 2048: 28 us with split-K narrow tiles,
+//    15.7 us with 2 waves of 64 x 64 and 64-byte stages, 12.1 us now);
 //  * kNarrow: fewer than 192 tiles and a longer K -- 128-token tiles, two
 //    workgroups per CU, plus split K (1024 x 2048 x 11008: 51 us, against 67 us
 //    for small tiles without a split).
@@ -1296,7 +1297,7 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
     case BigCfg::kWide:
       return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     case BigCfg::kSmall:
-      return launch_big<64, 128, 64, 2, 4, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      return launch_big<64, 128, 128, 2, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     default:
       return launch_big<128, 256, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
@@ -1316,7 +1317,7 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
   switch (pick_big(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0)) {
     case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
     case BigCfg::kWide: return big_plan(M, N, K, 256, 256, 128).ws_bytes;
-    case BigCfg::kSmall: return big_plan(M, N, K, 64, 128, 64).ws_bytes;
+    case BigCfg::kSmall: return big_plan(M, N, K, 64, 128, 128).ws_bytes;
     default: return big_plan(M, N, K, 128, 256, 64).ws_bytes;
   }
 }
