@@ -1267,9 +1267,10 @@ inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; 
 //    per wave: the loop is latency-bound at these sizes), two workgroups per
 //    CU, usually no split (1024 x 2560 x 2048: 28 us with split-K narrow tiles,
 //    15.7 us with 2 waves of 64 x 64 and 64-byte stages, 12.1 us now);
-//  * kNarrow: fewer than 192 tiles and a longer K -- 128-token tiles, two
-//    workgroups per CU, plus split K (1024 x 2048 x 11008: 51 us, against 67 us
-//    for small tiles without a split).
+//  * kNarrow: fewer than 192 tiles and a longer K -- 128 tokens x 256 weight
+//    rows, 8 waves of 128 x 32, 128-byte stages, one workgroup per CU, plus
+//    split K (1024 x 2048 x 11008: 41 us; 44 us with 4 waves of 128 x 64 and
+//    64-byte stages, 67 us for small tiles without a split).
 enum class BigCfg { kWide, kWide192, kSmall, kNarrow };
 
 inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
@@ -1299,7 +1300,7 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
     case BigCfg::kSmall:
       return launch_big<64, 128, 128, 2, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     default:
-      return launch_big<128, 256, 64, 3, 2, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      return launch_big<128, 256, 128, 2, 1, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
 }
 
@@ -1318,7 +1319,7 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
     case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
     case BigCfg::kWide: return big_plan(M, N, K, 256, 256, 128).ws_bytes;
     case BigCfg::kSmall: return big_plan(M, N, K, 64, 128, 128).ws_bytes;
-    default: return big_plan(M, N, K, 128, 256, 64).ws_bytes;
+    default: return big_plan(M, N, K, 128, 256, 128).ws_bytes;
   }
 }
 
