@@ -150,6 +150,22 @@ def test_large_m_epilogue_combinations(gpu, oracle_mod, act, res, gate):
     _check(gpu, oracle_mod, qa, sa, w, f"{act} res={res} gate={gate}", ref_w=fw, act=act, residual=r, gate=gt)
 
 
+@pytest.mark.parametrize("K", [1024, 8192])
+@pytest.mark.parametrize("act,resgate", [("gelu_tanh", False), (None, True), ("swiglu", False)])
+def test_ragged_small_grid_configs(gpu, oracle_mod, K, act, resgate):
+    # outputs of fewer than 192 256x256 tiles: 128x64 tiles for K <= 4096, split-K
+    # 256x128 tiles above; M and N end inside a tile
+    from instinctflash_amd.kernels import pack_glu
+    M, N = 333, 1056
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=K + M, bias=True)
+    glu = act == "swiglu"
+    n_out = N // 2 if glu else N
+    r = torch.randn((M, n_out), generator=g).to(torch.bfloat16) if resgate else None
+    gt = torch.rand(n_out, generator=g).to(torch.bfloat16) if resgate else None
+    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if glu else fw, f"ragged {act} K={K}", ref_w=fw, act=act,
+           residual=r, gate=gt)
+
+
 def test_fp32_output(gpu, oracle_mod):
     qa, sa, fw, _ = _make(gpu, 100, 512, 512, seed=8, bias=True)
     o32, _ = _check(gpu, oracle_mod, qa, sa, fw, "f32 out")
