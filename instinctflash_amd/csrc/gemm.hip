@@ -866,12 +866,13 @@ struct SkSplit {
 };
 
 struct SkinnyPlan {
-  int mb;          // 16-token blocks (1..4)
+  int mb;          // 16-token blocks per workgroup (1..4)
   int nbw;         // 16-row weight blocks per workgroup (1, or 2 for GLU)
   int64_t groups;  // row groups
   int ksplit;      // K slices per group (one workgroup each)
   int64_t kss;     // K steps per slice
   int waves;       // waves per workgroup (4, 8 or 16)
+  int tsplit;      // workgroups along the tokens per group (each owns mb blocks)
   size_t ws_bytes; // workspace (tickets + partials) when ksplit > 1
 };
 
@@ -895,6 +896,17 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   if (s < 1 || p.groups > kSkMaxGroups) s = 1;
   p.kss = (ksteps + s - 1) / s;
   p.ksplit = static_cast<int>((ksteps + p.kss - 1) / p.kss);
+  // One token block per workgroup (grid.y over the blocks) when the row groups
+  // alone leave CUs idle: the extra reads of each weight fragment hit L2, and
+  // each workgroup's MFMA and load chain gets 1/mb as long. Measured (M = 50,
+  // weights streamed from HBM): 50x1024x4096 10.9 -> 5.8 us, 50x2560x1024
+  // 6.4 -> 4.9 us, 50x4096x1024 6.5 -> 5.6 us; GLU weights (32-row groups) and
+  // more than 256 groups lose (50x8192x1024 GeGLU 7.6 -> 9.1 us).
+  p.tsplit = 1;
+  if (p.ksplit == 1 && p.mb > 1 && p.nbw == 1 && p.groups <= 256) {
+    p.tsplit = p.mb;
+    p.mb = 1;
+  }
   // Enough waves that every wave has at most kSkUnroll K steps of its slice
   // (one batch of loads in flight); 16 waves leave 128 VGPRs each, enough
   // for one 16 x 16 block only.
@@ -942,6 +954,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const int64_t s_begin = slice * sp.kss;
   const int64_t s_end = min(s_begin + sp.kss, ksteps);
   const bool a_tiled = (e.flags & IFX_EPI_A_TILED) != 0;  // A in the skinny tile layout (lda unused)
+  const int64_t mb0 = static_cast<int64_t>(blockIdx.y) * MB;  // first 16-token block of this workgroup
 
   const uint8_t* wrow[NBW];
 #pragma unroll
@@ -949,14 +962,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const uint8_t* arow[MB];
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
-    int64_t m = j * 16 + frow;
+    int64_t m = (mb0 + j) * 16 + frow;
     m = m < e.M ? m : e.M - 1;  // rows past M are computed, never stored
     arow[j] = A + m * lda + g * 32;
   }
 
   // Epilogue operands of the lanes that will finish token block j = wave,
   // fetched now so their latency hides under the weight stream.
-  const int64_t m_epi = wave < MB ? wave * 16 + frow : e.M;
+  const int64_t m_epi = wave < MB ? (mb0 + wave) * 16 + frow : e.M;
   const int64_t mc = min(m_epi, e.M - 1);
   const int64_t c_epi = NBW == 2 ? (nrow0 >> 5) * 16 + 4 * g : nrow0 + 4 * g;  // output column
   float sa_epi = 1.0f, sw_epi[NBW][4], b_epi[NBW][4], gate_epi[4] = {1.f, 1.f, 1.f, 1.f}, res_epi[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1019,7 +1032,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #else
         if (a_tiled) {  // workgroup-uniform
           const bool in = s < s_end;
-          const uint8_t* t = A + (j * ksteps + s) * 2048 + lane * 16;
+          const uint8_t* t = A + ((mb0 + j) * ksteps + s) * 2048 + lane * 16;
           af[u][j] = cat8(in ? ld16(t) : v4i{0, 0, 0, 0}, in ? ld16(t + 1024) : v4i{0, 0, 0, 0});
         } else {
           af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
@@ -1176,7 +1189,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
 template <int MB, int NBW, int WAVES>
 void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
                      const Epi& e, const SkSplit& sp, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit)), block(WAVES * 64);
+  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit), static_cast<unsigned>(p.tsplit)), block(WAVES * 64);
   if (e.flags & IFX_EPI_W_TILED)
     hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, true>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
   else
