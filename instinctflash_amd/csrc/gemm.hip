@@ -900,10 +900,11 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   // alone leave CUs idle: the extra reads of each weight fragment hit L2, and
   // each workgroup's MFMA and load chain gets 1/mb as long. Measured (M = 50,
   // weights streamed from HBM): 50x1024x4096 10.9 -> 5.8 us, 50x2560x1024
-  // 6.4 -> 4.9 us, 50x4096x1024 6.5 -> 5.6 us; GLU weights (32-row groups) and
-  // more than 256 groups lose (50x8192x1024 GeGLU 7.6 -> 9.1 us).
+  // 6.4 -> 4.9 us; GLU weights (32-row groups) and 256 or more groups lose or
+  // break even (50x8192x1024 GeGLU 7.6 -> 9.1 us; 50x4096x1024 with its
+  // weights L2/MALL-resident 4.7 -> 4.9 us, streamed from HBM 6.5 -> 5.6 us).
   p.tsplit = 1;
-  if (p.ksplit == 1 && p.mb > 1 && p.nbw == 1 && p.groups <= 256) {
+  if (p.ksplit == 1 && p.mb > 1 && p.nbw == 1 && p.groups < 256) {
     p.tsplit = p.mb;
     p.mb = 1;
   }
