@@ -126,8 +126,13 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
   constexpr int kDP = 32 * DT;        // padded head dim of V^T / O
   constexpr int kKPitch = kDP + 8;    // bf16 elements per K row (pitch 4 dwords off a bank multiple)
   constexpr int kVPitch = kDP + 16;   // per V row (8 dwords off: 4 rows x 32 bytes of a transposing read)
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBlockN * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kBlockN * kVPitch];
+  // K and V blocks; after the key loop the same memory stages the partial rows
+  constexpr int kTp = 36;  // floats per transpose row (32 + 4: rows start in different banks)
+  constexpr int kKV = kBlockN * (kKPitch + kVPitch);
+  constexpr int kTr = 4 * 32 * kTp * 2;  // 4 waves x 32 x kTp floats, in 16-bit units
+  __shared__ __attribute__((aligned(16))) uint16_t kv_lds[kKV > kTr ? kKV : kTr];
+  uint16_t* const k_lds = kv_lds;
+  uint16_t* const v_lds = kv_lds + kBlockN * kKPitch;
   __shared__ int s_end[4];
   __shared__ int s_min[4];
 
@@ -338,22 +343,37 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (!row_ok) return;
   if (a.splits > 1) {
-    const int64_t prow = ((static_cast<int64_t>(split) * gridDim.z + b) * a.Hkv + kvh) * a.n_rows + row;
-    if (half == 0) {
-      a.pm[prow] = m_run;
-      a.pl[prow] = l_tot;
+    // Partial rows leave through LDS, 32 head dims at a time: each wave writes
+    // its 32 x 32 fp32 block there (lane = query row) and stores it back
+    // row-major, so a store instruction covers 8 rows x 128 contiguous bytes
+    // instead of 32 rows x 32 bytes. The block buffers are free after the loop.
+    const int64_t wrow0 = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + wave * 32;
+    const int64_t pbase = ((static_cast<int64_t>(split) * gridDim.z + b) * a.Hkv + kvh) * a.n_rows;
+    if (row_ok && half == 0) {
+      a.pm[pbase + row] = m_run;
+      a.pl[pbase + row] = l_tot;
     }
-    float* po = a.po + prow * kDP;
+    float* tb = reinterpret_cast<float*>(kv_lds) + wave * 32 * kTp;
+    const int sr = lane >> 3, sc = 4 * (lane & 7);  // store: rows sr + 8k, floats sc..sc+3
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+    for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4*>(po + 32 * dt + 8 * q + 4 * half) =
+        *reinterpret_cast<float4*>(tb + col * kTp + 8 * q + 4 * half) =
             make_float4(acc[dt][4 * q], acc[dt][4 * q + 1], acc[dt][4 * q + 2], acc[dt][4 * q + 3]);
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = *reinterpret_cast<const float4*>(tb + (sr + 8 * k) * kTp + sc);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t r = wrow0 + sr + 8 * k;
+        if (r < a.n_rows) *reinterpret_cast<float4*>(a.po + (pbase + r) * kDP + 32 * dt + sc) = v[k];
+      }
+    }
     return;
   }
+  if (!row_ok) return;
   const float inv = 1.0f / l_tot;
   uint16_t* orow = a.o + b * a.sob + tok * a.sot + head * a.soh;
 #pragma unroll
