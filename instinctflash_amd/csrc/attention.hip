@@ -151,6 +151,18 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
   const int64_t tok = row_ok ? row / a.group : 0;
   const int head = kvh * a.group + static_cast<int>(row_ok ? row % a.group : 0);
 
+  // Q^T fragments (MFMA B operand): query `col`, dims 16c + 8*half .. +7;
+  // issued first, their latency overlaps the key-range reduction below
+  u32x4_t qf[2 * DT];
+#pragma unroll
+  for (int c = 0; c < 2 * DT; ++c) {
+    const int d = 16 * c + 8 * half;
+    if (row_ok && d < D)
+      qf[c] = *reinterpret_cast<const u32x4_t*>(a.q + b * a.sqb + tok * a.sqt + head * a.sqh + d);
+    else
+      qf[c] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+
   // visible keys of this row; the workgroup's key range [start, end) and the
   // bound below which every row sees every key (blocks under it skip masking)
   int lim = 0;
@@ -176,17 +188,6 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
     const int per = ((end + a.splits - 1) / a.splits + kBlockN - 1) / kBlockN * kBlockN;
     start = split * per;
     end = min(end, start + per);
-  }
-
-  // Q^T fragments (MFMA B operand): query `col`, dims 16c + 8*half .. +7
-  u32x4_t qf[2 * DT];
-#pragma unroll
-  for (int c = 0; c < 2 * DT; ++c) {
-    const int d = 16 * c + 8 * half;
-    if (row_ok && d < D)
-      qf[c] = *reinterpret_cast<const u32x4_t*>(a.q + b * a.sqb + tok * a.sqt + head * a.sqh + d);
-    else
-      qf[c] = u32x4_t{0u, 0u, 0u, 0u};
   }
 
   v16f acc[DT];
