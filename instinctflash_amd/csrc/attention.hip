@@ -30,6 +30,8 @@
 //                       gfx950 transposing LDS read ds_read_b64_tr_b16)
 // keeping O^T in registers (lane = query, 16 head dims per 32-dim tile).
 
+#include <type_traits>
+
 #include "ifx_abi.h"
 #include "ifx_device.h"
 #include "ifx_quant.h"
@@ -400,12 +402,12 @@ constexpr int kCombineMaxW = 1024;  // Hq * splits
 
 // ks > 0: q8 in the skinny tile layout (ks K steps; the grid covers 16*ceil(Tq/16)
 // token rows and the padding rows / K padding are written as zeros).
-template <bool BF16>
-__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, int64_t kdp, int64_t Hq,
+template <bool BF16, int NT>
+__global__ __launch_bounds__(NT) void attn_combine_kernel(AttnArgs a, int64_t kdp, int64_t Hq,
                                                                     uint8_t* q8, int64_t ldq8, float* q8s, int64_t ks,
                                                                     int64_t Tq) {
   using MF = Mfma<BF16>;
-  __shared__ uint32_t red[kAttnThreads / 64];
+  __shared__ uint32_t red[NT / 64];
   __shared__ float wgt[kCombineMaxW];
   const int64_t b = blockIdx.x;
   const int64_t tok = blockIdx.y;
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   const int S = a.splits;
   const int H = static_cast<int>(Hq);
   if (tok >= Tq) {  // tile-layout padding row (workgroup-uniform)
-    for (int64_t i = threadIdx.x; i < ks * 16; i += kAttnThreads)
+    for (int64_t i = threadIdx.x; i < ks * 16; i += NT)
       *reinterpret_cast<uint2*>(q8 + tile_offset(tok, 8 * i, ks)) = make_uint2(0u, 0u);
     return;
   }
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   // per (head, split): the partial row's index, its softmax state in LDS
   __shared__ float pl_s[kCombineMaxW];
   __shared__ int64_t off_s[kCombineMaxW];
-  for (int i = threadIdx.x; i < H * S; i += kAttnThreads) {
+  for (int i = threadIdx.x; i < H * S; i += NT) {
     const int h = i / S, sp = i - (i / S) * S;
     const int64_t pr = ((sp * nb + b) * a.Hkv + h / a.group) * a.n_rows + tok * a.group + h % a.group;
     off_s[i] = pr * kdp;
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   }
   __syncthreads();
   // per head: the max over splits, then the normalized split weights
-  for (int h = threadIdx.x; h < H; h += kAttnThreads) {
+  for (int h = threadIdx.x; h < H; h += NT) {
     float m = -__builtin_inff();
     for (int sp = 0; sp < S; ++sp) m = fmaxf(m, wgt[h * S + sp]);
     float l = 0.0f;
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   uint32_t amax = 0;
 #pragma unroll
   for (int j = 0; j < kG; ++j) {
-    const int e4 = threadIdx.x + j * kAttnThreads;
+    const int e4 = threadIdx.x + j * NT;
     val[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (e4 >= groups) continue;
     const int h = (4 * e4) / D, d = 4 * e4 - h * D;
@@ -486,12 +488,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
   __syncthreads();
   amax = red[0];
 #pragma unroll
-  for (int w = 1; w < kAttnThreads / 64; ++w) amax = amax > red[w] ? amax : red[w];
+  for (int w = 1; w < NT / 64; ++w) amax = amax > red[w] ? amax : red[w];
   const float sc = scale_from_amax_bits(amax);
   if (threadIdx.x == 0) q8s[tok] = sc;
 #pragma unroll
   for (int j = 0; j < kG; ++j) {
-    const int e4 = threadIdx.x + j * kAttnThreads;
+    const int e4 = threadIdx.x + j * NT;
     if (e4 < groups) {
       uint8_t* qp = ks > 0 ? q8 + tile_offset(tok, 4 * e4, ks) : q8 + tok * ldq8 + 4 * e4;
       qp[0] = static_cast<uint8_t>(q1(val[j].x, sc));
@@ -501,7 +503,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a, 
     }
   }
   if (ks > 0)  // K padding of the tile layout
-    for (int64_t i = groups / 2 + threadIdx.x; i < ks * 16; i += kAttnThreads)
+    for (int64_t i = groups / 2 + threadIdx.x; i < ks * 16; i += NT)
       *reinterpret_cast<uint2*>(q8 + tile_offset(tok, 8 * i, ks)) = make_uint2(0u, 0u);
 }
 
@@ -613,12 +615,27 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
   else dispatch_attn<false>(a, B, dt, st);
   if (splits > 1) {
     const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(q8_ks > 0 ? (Tq + 15) / 16 * 16 : Tq));
-    if (bf)
-      hipLaunchKernelGGL((attn_combine_kernel<true>), grid, dim3(kAttnThreads), 0, st, a, int64_t(32 * dt), Hq,
+    // Few tokens (fewer workgroups than CUs): one 4-dim group per lane, so more
+    // of the partial rows (written by other XCDs) are in flight per CU
+    // (pi05 chunk, 51 tokens: 18.8 -> 18.2 us); many tokens: 256 lanes (the
+    // 800-token prefix is 4.6 us slower with 512).
+    const int64_t groups = B * Tq < 128 ? Hq * D / 4 : 0;
+    auto launch = [&](auto bf_tag, auto nt_tag) {
+      constexpr bool kBf = decltype(bf_tag)::value;
+      constexpr int kNt = decltype(nt_tag)::value;
+      hipLaunchKernelGGL((attn_combine_kernel<kBf, kNt>), grid, dim3(kNt), 0, st, a, int64_t(32 * dt), Hq,
                          static_cast<uint8_t*>(q8), ldq8, q8_scale, q8_ks, Tq);
-    else
-      hipLaunchKernelGGL((attn_combine_kernel<false>), grid, dim3(kAttnThreads), 0, st, a, int64_t(32 * dt), Hq,
-                         static_cast<uint8_t*>(q8), ldq8, q8_scale, q8_ks, Tq);
+    };
+    using std::integral_constant;
+    if (bf) {
+      if (groups > 512) launch(integral_constant<bool, true>{}, integral_constant<int, 1024>{});
+      else if (groups > 256) launch(integral_constant<bool, true>{}, integral_constant<int, 512>{});
+      else launch(integral_constant<bool, true>{}, integral_constant<int, 256>{});
+    } else {
+      if (groups > 512) launch(integral_constant<bool, false>{}, integral_constant<int, 1024>{});
+      else if (groups > 256) launch(integral_constant<bool, false>{}, integral_constant<int, 512>{});
+      else launch(integral_constant<bool, false>{}, integral_constant<int, 256>{});
+    }
   }
   return launch_status();
 }
