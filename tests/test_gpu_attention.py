@@ -60,8 +60,10 @@ def test_causal_and_extra(gpu, oracle_mod):
     _close(out, _ref(oracle_mod, q, k, v, 30 + extra.numpy()), torch.float16, "extra")
 
 
-@pytest.mark.parametrize("hd,hq,hkv,splits", [(256, 8, 1, 3), (128, 16, 2, 2), (72, 16, 16, 4)])
+@pytest.mark.parametrize("hd,hq,hkv,splits", [(256, 8, 1, 3), (128, 16, 2, 2), (72, 16, 16, 4), (128, 40, 8, 5),
+                                              (32, 4, 1, 2)])
 def test_split_with_fused_quant(gpu, oracle_mod, hd, hq, hkv, splits):
+    # combine widths: 1280 / 512 / 288 / 32 four-dim groups per token row
     # tests/test_gi_kernels.py:157-176
     from instinctflash_amd.kernels import SplitWorkspace, attention
     T = 50
