@@ -386,27 +386,6 @@ __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __re
 // The barrier is the bare s_barrier: a __syncthreads() fence would also wait
 // for the loads that are meant to stay in flight.
 
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-// LDS byte offset of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)(p)));
-}
-
-// One global_load_lds_dwordx4: 64 lanes x 16 bytes from `src` (per lane) into
-// the 1 KB LDS block at byte offset `lds` (wave-uniform, via M0). Written as
-// inline asm on purpose: the compiler does not know this instruction writes
-// LDS, so it does not put an s_waitcnt vmcnt(0) in front of every later LDS
-// read "in case they alias" -- that wait would also drain the loads of the
-// stages that are meant to stay in flight. The kernel orders the DMA and the
-// LDS reads itself (s_waitcnt vmcnt(N) + s_barrier before each stage is read;
-// vector-memory loads complete in issue order, so the compiler's own vmcnt
-// counts for other loads stay conservative).
-__device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
-}
-
-
 // LDS layout of a tile with KB-byte rows: 16-byte chunk `ch` of row `row` is
 // stored at chunk position ch ^ f(row). gfx950's LDS serves a ds_read_b128 16
 // lanes at a time from 64 banks (a 256-byte window); a fragment read puts 16
@@ -475,13 +454,6 @@ struct Partials {
 __device__ __forceinline__ v16f mfma32(const v8i& w, const v8i& a, const v16f& c) {
   // cbsz = blgp = 0: both operands FP8 E4M3 (OCP); no block scales.
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, 0, 0, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) for a compile-time N (0..63).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ v4f quad(const v16f& v, int q) {

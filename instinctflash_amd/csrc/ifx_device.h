@@ -127,6 +127,34 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
          (__uint_as_float(row_lane(b, 32)) + __uint_as_float(row_lane(b, 48)));
 }
 
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// LDS byte offset of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)(p)));
+}
+
+// One global_load_lds_dwordx4: 64 lanes x 16 bytes from `src` (per lane) into
+// the 1 KB LDS block at byte offset `lds` (wave-uniform, via M0). Written as
+// inline asm on purpose: the compiler does not know this instruction writes
+// LDS, so it does not put an s_waitcnt vmcnt(0) in front of every later LDS
+// read "in case they alias" -- that wait would also drain the loads of the
+// stages that are meant to stay in flight. The caller orders the DMA and the
+// LDS reads itself (s_waitcnt vmcnt(N) + s_barrier before each stage is read;
+// vector-memory loads complete in issue order, so the compiler's own vmcnt
+// counts for other loads stay conservative).
+__device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+}
+
+
+// s_waitcnt vmcnt(N) for a compile-time N (0..63).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // GELU, tanh form: 0.5*x*(1+tanh(u)), u = sqrt(2/pi)*(x + 0.044715 x^3).
 // Since 0.5*(1+tanh(u)) = 1/(1+e^{-2u}), this is x / (1 + 2^z) with
 // z = -2u*log2(e) = x*(a + b*x^2): one FMA-based polynomial, one exp2 and one

@@ -92,7 +92,9 @@ def test_split_with_fused_quant(gpu, oracle_mod, hd, hq, hkv, splits):
 
 @pytest.mark.parametrize("B,Tq,Tk,hq,hkv,hd,splits", [(1, 800, 800, 8, 1, 256, 1), (2, 51, 900, 8, 1, 256, 4),
                                                       (1, 1, 2000, 16, 2, 128, 8), (3, 17, 130, 12, 4, 64, 1),
-                                                      (1, 33, 65, 4, 4, 96, 2), (1, 5, 7, 2, 1, 32, 1)])
+                                                      (1, 33, 65, 4, 4, 96, 2), (1, 5, 7, 2, 1, 32, 1),
+                                                      (1, 40, 300, 4, 2, 160, 3), (1, 33, 129, 2, 1, 200, 1),
+                                                      (2, 17, 70, 4, 4, 224, 2), (1, 70, 1, 8, 1, 256, 1)])
 def test_shapes_bf16(gpu, oracle_mod, B, Tq, Tk, hq, hkv, hd, splits):
     from instinctflash_amd.kernels import SplitWorkspace, attention
     q, k, v = _qkv(B, Tq, Tk, hq, hkv, hd, Tq + Tk, torch.bfloat16)
