@@ -269,6 +269,31 @@ int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* ro
                   int64_t HD, void* stream);
 
 /*
+ * FP8 QKV projection with the qkv_split work in the GEMM's epilogue (M <= 64):
+ *   y = a . w^T * sa[m] * sw[n] (+ bias[n])           (fp32, never rounded to bf16)
+ *   Q, K heads: rotary on pairs (i, i + HD/2), angle = pos[t * ldpos] * inv_freq[i]
+ *   Q at q_out[t*sq_t + h*sq_h + d]; K / V at k_out / v_out[(kv_base + t)*s*_t + h*s*_h + d]
+ * w [N = (heads_q + 2*heads_kv) * head_dim, K] has its rows reordered per head:
+ * packed row 16k + 4g + r of a head holds head dim d + (r & 1) + (r >= 2 ? HD/2 : 0),
+ * d = 8k + 2g (sw and bias in the same order); it may then be tiled
+ * (IFX_EPI_W_TILED, ifx_fp8_pack_skinny). flags: IFX_EPI_BIAS, IFX_EPI_W_TILED,
+ * IFX_EPI_A_TILED only. head_dim % 16 == 0, <= 256; inv_freq NULL = no rotation;
+ * kv_base_dev: NULL or a device int32 read in place of kv_base; out_dtype BF16, F16
+ * or F32. Workspace as ifx_fp8_linear(M, N, K, 0).
+ * Replaces: the pair ifx_fp8_linear (raw accumulator, reference
+ * instinctflash/kernels/fp8.py:50-53 `gemm`) + ifx_qkv_split (reference
+ * instinctflash/kernels/rope.py:89-116) at decode / action-chunk sizes; the
+ * reference has no single call for it.
+ */
+int ifx_fp8_linear_qkv_rope(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
+                            const float* sw, const float* bias, int flags, const float* pos, int64_t ldpos,
+                            const float* inv_freq, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                            void* q_out, int64_t sq_t, int64_t sq_h, void* k_out, int64_t sk_t, int64_t sk_h,
+                            void* v_out, int64_t sv_t, int64_t sv_h, int out_dtype, int64_t kv_base,
+                            const int32_t* kv_base_dev, int64_t M, int64_t K, void* workspace, size_t ws_bytes,
+                            void* stream);
+
+/*
  * Wan DiT QKV consumer: raw [rows, parts * D] (BF16 or F32, D = heads * head_dim,
  * parts = 1 + (k_pool != NULL) + (v_pool != NULL): Q, then K, then V columns):
  *   x = raw * row[r] * col + bias               (per part, columns of that part)

@@ -92,6 +92,9 @@ SIGNATURES = {
     "ifx_fp8_linear": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64,
                               _I64, _I64, _P, _SZ, _P]),
     "ifx_fp8_pack_glu": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P]),
+    "ifx_fp8_linear_qkv_rope": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _INT, _P, _I64, _P, _I64, _I64, _I64,
+                                       _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _INT, _I64, _P,
+                                       _I64, _I64, _P, _SZ, _P]),
 }
 
 _lock = threading.Lock()

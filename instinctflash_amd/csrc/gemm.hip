@@ -830,11 +830,75 @@ constexpr int kSkUnroll = 4;       // K steps whose loads are issued together pe
 constexpr int kSkMaxGroups = 256;  // row groups that may split K (one ticket each)
 constexpr size_t kWsHeader = kSkMaxGroups * sizeof(int);  // tickets at the workspace start
 
+// The qkv_split epilogue of ifx_fp8_linear_qkv_rope (flag kEpiRopeQkv): the
+// fused q|k|v weight rows are permuted per head so that packed rows
+// 16k + 4g + {0, 1, 2, 3} hold head dims d, d + 1, d + HD/2, d + 1 + HD/2
+// with d = 8k + 2g; the lane that owns those four outputs of a token applies
+// the rotary pairs (d, d + HD/2) and (d + 1, d + 1 + HD/2) itself.
+constexpr int kEpiRopeQkv = 1 << 20;  // internal flag, never accepted from callers
+
+struct RopeQkv {
+  const float* pos;       // position of token m at pos[m * ldpos]
+  int64_t ldpos;
+  const float* inv_freq;  // [HD/2] or null (no rotation)
+  int64_t hq, hkv, hd;
+  void* q;                // Q at q[m*sq_t + h*sq_h + d]
+  int64_t sq_t, sq_h;
+  void* k;                // K at k[(kv_base + m)*sk_t + h*sk_h + d]
+  int64_t sk_t, sk_h;
+  void* v;                // V likewise
+  int64_t sv_t, sv_h;
+  int64_t kv_base;
+  const int32_t* kv_base_dev;  // device kv_base, or null
+  int out_dtype;               // IFX_DTYPE_F16 / BF16 / F32
+};
+
+__device__ __forceinline__ void store_elem(int dtype, void* base, int64_t i, float v) {
+  if (dtype == IFX_DTYPE_F32) static_cast<float*>(base)[i] = v;
+  else if (dtype == IFX_DTYPE_F16) static_cast<_Float16*>(base)[i] = static_cast<_Float16>(v);
+  else static_cast<__bf16*>(base)[i] = static_cast<__bf16>(v);
+}
+
+// y = the four outputs of token m at packed columns p .. p + 3 (p % 4 == 0).
+__device__ __forceinline__ void rope_qkv_store(const RopeQkv& r, int64_t m, int64_t p, const float* y) {
+  const int64_t head = p / r.hd, pq = p - head * r.hd, half = r.hd / 2;
+  const int64_t d = 8 * (pq / 16) + 2 * ((pq % 16) / 4);
+  float lo0 = y[0], lo1 = y[1], hi0 = y[2], hi1 = y[3];
+  if (r.inv_freq && head < r.hq + r.hkv) {  // Q and K heads rotate
+    const float ps = r.pos[m * r.ldpos];
+    float s0, c0, s1, c1;
+    sincosf(ps * r.inv_freq[d], &s0, &c0);
+    sincosf(ps * r.inv_freq[d + 1], &s1, &c1);
+    rotate_pair(lo0, hi0, c0, s0);
+    rotate_pair(lo1, hi1, c1, s1);
+  }
+  void* dst;
+  int64_t off;
+  if (head < r.hq) {
+    dst = r.q;
+    off = m * r.sq_t + head * r.sq_h;
+  } else {
+    const int64_t krow = (r.kv_base_dev ? static_cast<int64_t>(*r.kv_base_dev) : r.kv_base) + m;
+    if (head < r.hq + r.hkv) {
+      dst = r.k;
+      off = krow * r.sk_t + (head - r.hq) * r.sk_h;
+    } else {
+      dst = r.v;
+      off = krow * r.sv_t + (head - r.hq - r.hkv) * r.sv_h;
+    }
+  }
+  store_elem(r.out_dtype, dst, off + d, lo0);
+  store_elem(r.out_dtype, dst, off + d + 1, lo1);
+  store_elem(r.out_dtype, dst, off + half + d, hi0);
+  store_elem(r.out_dtype, dst, off + half + d + 1, hi1);
+}
+
 struct SkSplit {
   float* part;     // [ksplit][groups][NBW][MB][64 lanes] x 4 floats
   int* tickets;    // [groups], zero between calls
   int ksplit;
   int64_t kss;     // K steps per slice
+  RopeQkv rope;    // the qkv_split epilogue's arguments (flag kEpiRopeQkv)
 };
 
 struct SkinnyPlan {
@@ -1087,7 +1151,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
       if (e.flags & IFX_EPI_GATE) y[r] = mul_rn(y[r], gate_epi[r]);
       if (e.flags & IFX_EPI_RESIDUAL) y[r] = res_epi[r] + y[r];
     }
-    epi_store4(e, m_epi, c_epi, y);
+    if (NBW == 1 && (e.flags & kEpiRopeQkv)) rope_qkv_store(sp.rope, m_epi, c_epi, y);
+    else epi_store4(e, m_epi, c_epi, y);
   }
 }
 
@@ -1191,8 +1256,8 @@ void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const 
 
 template <int NBW>
 int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                  const Epi& e, void* ws, size_t ws_bytes, hipStream_t st) {
-  SkSplit sp{nullptr, nullptr, p.ksplit, p.kss};
+                  const Epi& e, void* ws, size_t ws_bytes, hipStream_t st, const RopeQkv* rope = nullptr) {
+  SkSplit sp{nullptr, nullptr, p.ksplit, p.kss, rope ? *rope : RopeQkv{}};
   if (p.ksplit > 1) {
     if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
     sp.tickets = static_cast<int*>(ws);
@@ -1396,6 +1461,40 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
+}
+
+int ifx_fp8_linear_qkv_rope(const void* a, int64_t lda, const float* sa, const void* w, int64_t ldw,
+                            const float* sw, const float* bias, int flags, const float* pos, int64_t ldpos,
+                            const float* inv_freq, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                            void* q_out, int64_t sq_t, int64_t sq_h, void* k_out, int64_t sk_t, int64_t sk_h,
+                            void* v_out, int64_t sv_t, int64_t sv_h, int out_dtype, int64_t kv_base,
+                            const int32_t* kv_base_dev, int64_t M, int64_t K, void* workspace, size_t ws_bytes,
+                            void* stream) {
+  constexpr int kAllowed = IFX_EPI_BIAS | IFX_EPI_W_TILED | IFX_EPI_A_TILED;
+  if (flags & ~kAllowed) return IFX_ERR_INVALID;
+  if (out_dtype != IFX_DTYPE_BF16 && out_dtype != IFX_DTYPE_F16 && out_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
+  if (heads_q <= 0 || heads_kv <= 0 || head_dim <= 0 || head_dim % 16 != 0 || kv_base < 0) return IFX_ERR_INVALID;
+  if (head_dim > 256) return IFX_ERR_UNSUPPORTED;
+  if (M > kSkinnyMaxM) return IFX_ERR_UNSUPPORTED;  // the register epilogue is the skinny kernel's
+  const int64_t N = (heads_q + 2 * heads_kv) * head_dim;
+  // check_linear validates the operands; the Q buffer stands in for `out`
+  // (its own layout is checked below)
+  const int rc = check_linear(w, ldw, sw, bias, nullptr, 0, nullptr, flags, q_out, N, M, N, K);
+  if (rc != IFX_OK) return rc;
+  const bool a_tiled = (flags & IFX_EPI_A_TILED) != 0;
+  if (!a_tiled && lda < K) return IFX_ERR_INVALID;
+  if (inv_freq && (!pos || ldpos < 1)) return IFX_ERR_INVALID;
+  if (sq_h < head_dim || sq_t < heads_q * sq_h || sk_h < head_dim || sv_h < head_dim) return IFX_ERR_INVALID;
+  if (sk_t < heads_kv * sk_h || sv_t < heads_kv * sv_h) return IFX_ERR_INVALID;
+  if (M == 0) return IFX_OK;
+  if (!a || !k_out || !v_out) return IFX_ERR_INVALID;
+  if (!aligned16(a) || (!a_tiled && lda % 16 != 0)) return IFX_ERR_ALIGN;
+  Epi e{sa, sw, bias, nullptr, 0, nullptr, q_out, N, flags | kEpiRopeQkv, M, N};
+  const RopeQkv r{pos, ldpos, inv_freq, heads_q, heads_kv, head_dim, q_out, sq_t, sq_h, k_out, sk_t, sk_h,
+                  v_out, sv_t, sv_h, kv_base, kv_base_dev, out_dtype};
+  const SkinnyPlan p = skinny_plan(M, N, K, false);
+  return launch_skinny<1>(p, static_cast<const uint8_t*>(a), lda, static_cast<const uint8_t*>(w), ldw, K, e,
+                          workspace, ws_bytes, static_cast<hipStream_t>(stream), &r);
 }
 
 size_t ifx_fp8_skinny_tiled_bytes(int64_t N, int64_t K) {

@@ -155,6 +155,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Rotary pair: (lo, hi) -> (lo*c - hi*s, hi*c + lo*s), each product rounded
+// on its own (no fused multiply-add), so every kernel that rotates a pair
+// produces the same bits.
+__device__ __forceinline__ void rotate_pair(float& lo, float& hi, float c, float s) {
+#pragma clang fp contract(off)
+  const float l = lo * c - hi * s;
+  const float h = hi * c + lo * s;
+  lo = l;
+  hi = h;
+}
+
 // GELU, tanh form: 0.5*x*(1+tanh(u)), u = sqrt(2/pi)*(x + 0.044715 x^3).
 // Since 0.5*(1+tanh(u)) = 1/(1+e^{-2u}), this is x / (1 + 2^z) with
 // z = -2u*log2(e) = x*(a + b*x^2): one FMA-based polynomial, one exp2 and one

@@ -203,11 +203,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_split_kernel(QkvArgs 
       }
       if (a.inv_freq) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float rlo = lo[j] * cs[j] - hi[j] * sn[j];
-          hi[j] = hi[j] * cs[j] + lo[j] * sn[j];
-          lo[j] = rlo;
-        }
+        for (int j = 0; j < NJ; ++j) rotate_pair(lo[j], hi[j], cs[j], sn[j]);
       }
     }
     void* dst;

@@ -35,6 +35,9 @@ class Fp8Weight:
     weight already repacked by :func:`pack_glu` (rows interleaved in blocks of 16).
     ``tiled`` marks a weight repacked by :func:`pack_skinny` for M <= 64 calls:
     ``w`` then holds 2 KB fragment tiles and ``nk`` the logical (N, K).
+    ``rope`` = (heads_q, heads_kv, head_dim) marks a fused q|k|v weight whose
+    rows were reordered by :func:`~instinctflash_amd.kernels.rope.permute_rope_rows`
+    for :func:`~instinctflash_amd.kernels.rope.linear_qkv_rope` only.
     """
 
     w: torch.Tensor
@@ -43,6 +46,7 @@ class Fp8Weight:
     glu: bool = False
     tiled: bool = False
     nk: tuple | None = None
+    rope: tuple | None = None
 
     @property
     def shape(self):
@@ -312,6 +316,8 @@ def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales
 
 
 def _linear(a, sa, w: Fp8Weight, out, flags, residual=None, gate=None, use_scales=True):
+    if w.rope is not None:
+        raise ValueError("this weight's rows are reordered for linear_qkv_rope; use that call")
     if isinstance(a, TiledRows):
         M, K, lda = a.M, a.K, 0
         _on_device("a", a.q)
@@ -450,4 +456,4 @@ def pack_skinny(w: Fp8Weight) -> Fp8Weight:
     lib = _lib.load()
     out = torch.empty(lib.ifx_fp8_skinny_tiled_bytes(N, K), dtype=E4M3, device=w.w.device)
     _lib.check(lib.ifx_fp8_pack_skinny(_ptr(w.w), ldw, N, K, _ptr(out), _stream(w.w.device)), "ifx_fp8_pack_skinny")
-    return Fp8Weight(out, w.scale, w.bias, glu=w.glu, tiled=True, nk=(N, K))
+    return Fp8Weight(out, w.scale, w.bias, glu=w.glu, tiled=True, nk=(N, K), rope=w.rope)
