@@ -194,7 +194,7 @@ def measure_engine(dev, reps=5):
     graph = capture(lambda i: eng.forward(), 1, side)
     time_graph(graph)
     ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    launches = 10 * (2 + 18 * 9)
+    launches = 10 * (2 + 18 * 8)
     _log(f"[bench] pi05 expert: {ms:.3f} ms per 50-action chunk ({launches} kernels + torch addmm)")
     return {"workload": "pi05 action expert, 10 steps x 18 layers, prefix 800, chunk 50 (random weights)",
             "ms_per_chunk": round(ms, 4), "kernels_per_chunk": launches}

@@ -19,9 +19,10 @@ head of 256), since no checkpoint is available here.
 operands, attention into fp16 then ``row_quant``). The default keeps the same
 math but lays the loop out for gfx950: weights in the skinny tile layout
 (``pack_skinny``), every FP8 activation written by its producer in the tile
-layout the M <= 64 GEMM reads with 1 KB loads, and the attention's split-KV
-combine emitting the output projection's FP8 operand directly (one kernel per
-layer fewer).
+layout the M <= 64 GEMM reads with 1 KB loads, the QKV split's rescale, rotary
+pairs and cache stores done in the QKV projection's epilogue
+(``linear_qkv_rope``), and the attention's split-KV combine emitting the output
+projection's FP8 operand directly (two kernels per layer fewer).
 """
 from __future__ import annotations
 
@@ -29,8 +30,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, pack_skinny, \
-    qkv_split, quantize_weight, residual_norm_quant, rope_inv_freq, row_quant
+from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, linear_qkv_rope, \
+    pack_skinny, permute_rope_rows, qkv_split, quantize_weight, residual_norm_quant, rope_inv_freq, row_quant
 from .kernels.activation import GELU_TANH
 from .kernels.attention import split_count
 
@@ -126,8 +127,8 @@ class Pi05Expert:
             tiled = lambda k: TiledRows(torch.zeros(lib.ifx_quant_rows_tiled_bytes(A, k), dtype=E4M3,  # noqa: E731
                                                     device=dev), A, k)
             self.xq, self.oq, self.hq = tiled(EX_D), tiled(HEADS * HEAD_DIM), tiled(EX_FF)
-            self.layers = [ExpertLayer(pack_skinny(L.qkv), pack_skinny(L.o), pack_skinny(L.gate_up),
-                                       pack_skinny(L.down)) for L in weights.layers]
+            self.layers = [ExpertLayer(pack_skinny(permute_rope_rows(L.qkv, HEADS, 1, HEAD_DIM)), pack_skinny(L.o),
+                                       pack_skinny(L.gate_up), pack_skinny(L.down)) for L in weights.layers]
             splits = max(2, split_count(1, A, HEADS, 1, self.smax + A))
             self.split = SplitWorkspace(1, A, HEADS, 1, HEAD_DIM, splits, dev)
 
@@ -203,10 +204,8 @@ class Pi05Expert:
             ma, mf = w.mod_attn[step], w.mod_ffn[step]
             residual_norm_quant(self.dx, mod_scale=ma[0, 0], mod_shift=ma[0, 1], q=xq, q_scale=s[0])
             for i, L in enumerate(self.layers):
-                gemm(xq, L.qkv, raw(A, QKV_N))
-                qkv_split(raw(A, QKV_N), self.q16[:A], self.kc[i], self.vc[i], heads_q=HEADS, heads_kv=1,
-                          head_dim=HEAD_DIM, inv_freq=self.inv_freq, pos=self.pos_chunk, row=s[0],
-                          col=L.qkv.scale, kv_base=self.prefix_len)
+                linear_qkv_rope(xq, s[0], L.qkv, self.q16[:A], self.kc[i], self.vc[i], inv_freq=self.inv_freq,
+                                pos=self.pos_chunk, kv_base=self.prefix_len)
                 attention(qv, self.kc[i][None], self.vc[i][None], kv_len=self.kv_len, scale=HEAD_DIM ** -0.5,
                           split=self.split, q8=oq, q8_scale=s[1])
                 gemm(oq, L.o, raw(A, EX_D))
