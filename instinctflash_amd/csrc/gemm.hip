@@ -944,6 +944,13 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
     p.tsplit = p.mb;
     p.mb = 1;
   }
+  // GLU weights with four token blocks: two workgroups of two blocks each
+  // (50x8192x1024 GeGLU 7.5 -> 6.5 us; one block each is slower, and so is
+  // splitting two blocks: 32x8192x2048 SwiGLU 7.5 -> 7.7 us).
+  if (p.ksplit == 1 && p.nbw == 2 && p.mb == 4 && p.groups <= 256) {
+    p.tsplit = 2;
+    p.mb = 2;
+  }
   // Enough waves that every wave has at most kSkUnroll K steps of its slice
   // (one batch of loads in flight); 16 waves leave 128 VGPRs each, enough
   // for one 16 x 16 block only.
