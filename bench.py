@@ -299,7 +299,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the FP8 projection path has no multi-GPU step in this build "
-              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(sharded, it would split each projection by output channels, one shard per GPU); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch

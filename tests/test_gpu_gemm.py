@@ -1,7 +1,7 @@
 """GPU parity of the FP8 GEMM + fused epilogue against the dequantize-then-fp32-matmul
 oracle (benchmarks/native/fp8_probe.py:36 in the reference).
 
-Acceptance: max|d| <= 2e-2 * rms(ref) and cosine >= 0.9999,
+Acceptance bar of the FP8 path: max|d| <= 2e-2 * rms(ref) and cosine >= 0.9999,
 for every epilogue and both kernel families (skinny M <= 64, LDS-tiled M > 64),
 including ragged M/N/K tails, strided operands, in-place residual and determinism.
 

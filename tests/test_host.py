@@ -107,7 +107,7 @@ def test_kernel_declarations():
 
 
 # ---------------------------------------------------------------------------
-# workload accounting (BASELINE.md section 2 / survey 8(d) byte model)
+# workload accounting (the per-config FLOP and byte model of the benchmark)
 # ---------------------------------------------------------------------------
 
 def test_workload_accounting_matches_published_table():
