@@ -159,7 +159,7 @@ def measure_producers(dev, launches=32):
             p.step()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        g = capture(lambda i: p.step(), launches, side)
+        g = capture(lambda i: p.step(i), launches, side)
         time_graph(g)
         us = sorted(time_graph(g)[0] / launches * 1e3 for _ in range(5))[2]
         gbs = p.bytes / us / 1e3

@@ -444,6 +444,44 @@ class QkvSplit:
                          sections=self.sec, kv_base=self.T // 2)
 
 
+class QkvRope:
+    """The pi05 expert's QKV projection with the QKV split in its epilogue
+    (``linear_qkv_rope``): 50 tokens x 1024 -> 8 query + 1 KV heads of 256,
+    rotary on Q and K, Q and the K/V cache rows in fp16, weights and activations
+    in the skinny tile layout (weights rotated through a pool larger than the
+    MALL, as 18 layers of them are in the engine). Algorithmic bytes: weights,
+    activations and scales read once, q/k/v written once."""
+
+    def __init__(self, dev, M=50, K=1024, HQ=8, HKV=1, HD=256, seed=0):
+        from .kernels import rope as R
+        self.R, self.M, self.K, self.HQ, self.HKV, self.HD = R, M, K, HQ, HKV, HD
+        g = _gen(seed)
+        N = (HQ + 2 * HKV) * HD
+        x = torch.randn(M, K, generator=g).to(dev)
+        self.xq, self.sa = F.quant_rows_tiled(x)
+        w = F.quantize_weight((torch.randn(N, K, generator=g) * 0.02).to(dev))
+        pool = max(1, (300 << 20) // (N * K))
+        self.ws = [F.pack_skinny(R.permute_rope_rows(F.Fp8Weight(w.w.clone(), w.scale.clone()), HQ, HKV, HD))
+                   for _ in range(pool)]
+        self.inv = R.rope_inv_freq(HD, 1e4, dev)
+        self.pos = (torch.arange(M, dtype=torch.float32) + 800).reshape(M, 1).to(dev)
+        self.base = torch.tensor([800], dtype=torch.int32, device=dev)
+        self.q = torch.empty(M, HQ, HD, dtype=torch.float16, device=dev)
+        self.kc = torch.empty(832 + M, HKV, HD, dtype=torch.float16, device=dev)
+        self.vc = torch.empty_like(self.kc)
+        self.title = (f"linear_qkv_rope {M}x{K} -> {HQ}+2x{HKV} heads x {HD} (FP8 projection + rotary + "
+                      f"KV-cache store, weight pool of {pool})")
+
+    @property
+    def bytes(self) -> int:
+        N = (self.HQ + 2 * self.HKV) * self.HD
+        return N * self.K + self.M * self.K + 4 * (self.M + N) + 2 * self.M * N
+
+    def step(self, i=0):
+        self.R.linear_qkv_rope(self.xq, self.sa, self.ws[i % len(self.ws)], self.q, self.kc, self.vc,
+                               inv_freq=self.inv, pos=self.pos, kv_base=self.base)
+
+
 class WanQkv:
     """``wan_qkv`` after the C5 qkv projection (Wan 5B: 24 heads of 128, bias,
     full-width q/k RMSNorm, 3-section interleaved rotary), Q dense, K/V into
@@ -583,5 +621,5 @@ class AttnPrefix(Attn):
 
 
 PRODUCERS = {"C5": (8192, 3072), "C2": (16, 1536)}
-CONSUMERS = {"C4": QkvSplit, "C5": WanQkv, "vla2 MoE": MoeRoute, "vla2 MoE act": MoeAct, "pi05 chunk": Attn,
-             "pi05 prefix": AttnPrefix}
+CONSUMERS = {"C4": QkvSplit, "C5": WanQkv, "pi05 qkv": QkvRope, "vla2 MoE": MoeRoute, "vla2 MoE act": MoeAct,
+             "pi05 chunk": Attn, "pi05 prefix": AttnPrefix}
