@@ -80,7 +80,7 @@ struct AttnArgs {
   const int32_t* kv_index;  // or null
   float qk_scale;           // scale * log2(e)
   int splits;
-  float* po;  // [splits, B, Hkv, n_rows, 32 * DT] raw partial outputs
+  uint16_t* po;  // [splits, B, Hkv, n_rows, 32 * DT] partial outputs / their own l, 16-bit (operand type)
   float* pm;  // [splits, B, Hkv, n_rows] running max (log2 domain)
   float* pl;  // [splits, B, Hkv, n_rows] softmax denominators
 };
@@ -347,31 +347,36 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   if (a.splits > 1) {
-    // Partial rows leave through LDS, 32 head dims at a time: each wave writes
-    // its 32 x 32 fp32 block there (lane = query row) and stores it back
-    // row-major, so a store instruction covers 8 rows x 128 contiguous bytes
-    // instead of 32 rows x 32 bytes. The block buffers are free after the loop.
+    // Partial rows are stored normalized by their own l, in the operands'
+    // 16-bit type (|O/l| <= max |V|; half the bytes of fp32 to write here and to
+    // read in the combine). They leave through LDS, 32 head dims at a time: each
+    // wave writes its 32 x 32 block there (lane = query row) and stores it back
+    // row-major, 16 rows x 64 contiguous bytes per store instruction instead of
+    // 32 rows x 16 bytes. The block buffers are free after the loop.
     const int64_t wrow0 = static_cast<int64_t>(blockIdx.x) * kRowsPerWg + wave * 32;
     const int64_t pbase = ((static_cast<int64_t>(split) * gridDim.z + b) * a.Hkv + kvh) * a.n_rows;
     if (row_ok && half == 0) {
       a.pm[pbase + row] = m_run;
       a.pl[pbase + row] = l_tot;
     }
-    float* tb = reinterpret_cast<float*>(kv_lds) + wave * 32 * kTp;
-    const int sr = lane >> 3, sc = 4 * (lane & 7);  // store: rows sr + 8k, floats sc..sc+3
+    constexpr int kTp16 = 20;  // 32-bit words per LDS row: 16 (32 dims) + 4 (16-byte aligned rows)
+    uint32_t* tb = reinterpret_cast<uint32_t*>(kv_lds) + wave * 32 * kTp16;
+    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int sr = lane >> 2, sc = 4 * (lane & 3);  // store: rows sr + 16k, words sc..sc+3 (dims 2sc..)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4*>(tb + col * kTp + 8 * q + 4 * half) =
-            make_float4(acc[dt][4 * q], acc[dt][4 * q + 1], acc[dt][4 * q + 2], acc[dt][4 * q + 3]);
-      float4 v[4];
+        *reinterpret_cast<u32x2_t*>(tb + col * kTp16 + 4 * q + 2 * half) =
+            u32x2_t{MF::pack2(acc[dt][4 * q] * inv_l, acc[dt][4 * q + 1] * inv_l),
+                    MF::pack2(acc[dt][4 * q + 2] * inv_l, acc[dt][4 * q + 3] * inv_l)};
+      u32x4_t v[2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = *reinterpret_cast<const float4*>(tb + (sr + 8 * k) * kTp + sc);
+      for (int k = 0; k < 2; ++k) v[k] = *reinterpret_cast<const u32x4_t*>(tb + (sr + 16 * k) * kTp16 + sc);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int64_t r = wrow0 + sr + 8 * k;
-        if (r < a.n_rows) *reinterpret_cast<float4*>(a.po + (pbase + r) * kDP + 32 * dt + sc) = v[k];
+      for (int k = 0; k < 2; ++k) {
+        const int64_t r = wrow0 + sr + 16 * k;
+        if (r < a.n_rows) *reinterpret_cast<u32x4_t*>(a.po + (pbase + r) * kDP + 32 * dt + 2 * sc) = v[k];
       }
     }
     return;
@@ -442,7 +447,8 @@ __global__ __launch_bounds__(NT) void attn_combine_kernel(AttnArgs a, int64_t kd
       l = l + w * pl_s[h * S + sp];
     }
     const float inv = 1.0f / l;
-    for (int sp = 0; sp < S; ++sp) wgt[h * S + sp] = wgt[h * S + sp] * inv;
+    // the stored partials are O_s / l_s: weight exp2(m_s - m) * l_s / l
+    for (int sp = 0; sp < S; ++sp) wgt[h * S + sp] = wgt[h * S + sp] * pl_s[h * S + sp] * inv;
   }
   __syncthreads();
   // the merged row in groups of 4 head dims; the partials of up to 16 splits of
@@ -463,7 +469,9 @@ __global__ __launch_bounds__(NT) void attn_combine_kernel(AttnArgs a, int64_t kd
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const int sp = min(s0 + u, S - 1);
-        pv[u] = *reinterpret_cast<const float4*>(a.po + off_s[h * S + sp] + d);
+        const u32x2_t r = *reinterpret_cast<const u32x2_t*>(a.po + off_s[h * S + sp] + d);
+        pv[u] = make_float4(MF::to_f32(static_cast<uint16_t>(r[0])), MF::to_f32(static_cast<uint16_t>(r[0] >> 16)),
+                            MF::to_f32(static_cast<uint16_t>(r[1])), MF::to_f32(static_cast<uint16_t>(r[1] >> 16)));
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
@@ -539,7 +547,7 @@ size_t ifx_attention_workspace_size(int64_t B, int64_t Tq, int64_t Hq, int64_t H
   if (B <= 0 || Tq <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D <= 0 || D > 256 || splits <= 1) return 0;
   const int64_t rows = static_cast<int64_t>(splits) * B * Hkv * Tq * (Hq / Hkv);
   const int64_t dp = (D + 31) / 32 * 32;
-  return static_cast<size_t>(rows * (dp + 2)) * sizeof(float);
+  return static_cast<size_t>(rows) * (dp * sizeof(uint16_t) + 2 * sizeof(float));
 }
 
 int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B, int64_t Tq,
@@ -605,8 +613,8 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
   a.splits = splits;
   if (splits > 1) {
     const int64_t rows = static_cast<int64_t>(splits) * B * Hkv * a.n_rows;
-    a.po = static_cast<float*>(workspace);
-    a.pm = a.po + rows * 32 * dt;
+    a.po = static_cast<uint16_t*>(workspace);
+    a.pm = reinterpret_cast<float*>(a.po + rows * 32 * dt);
     a.pl = a.pm + rows;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
