@@ -21,8 +21,11 @@ math but lays the loop out for gfx950: weights in the skinny tile layout
 (``pack_skinny``), every FP8 activation written by its producer in the tile
 layout the M <= 64 GEMM reads with 1 KB loads, the QKV split's rescale, rotary
 pairs and cache stores done in the QKV projection's epilogue
-(``linear_qkv_rope``), and the attention's split-KV combine emitting the output
-projection's FP8 operand directly (two kernels per layer fewer).
+(``linear_qkv_rope``), GeGLU in the gate|up projection's epilogue (GLU-packed
+weights, then ``row_quant`` of the half-width result instead of
+``gated_act_quant`` of the full-width accumulator), and the attention's split-KV
+combine emitting the output projection's FP8 operand directly (two kernels per
+layer fewer).
 """
 from __future__ import annotations
 
@@ -30,8 +33,9 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, linear_qkv_rope, \
-    pack_skinny, permute_rope_rows, qkv_split, quantize_weight, residual_norm_quant, rope_inv_freq, row_quant
+from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, linear, \
+    linear_qkv_rope, pack_glu, pack_skinny, permute_rope_rows, qkv_split, quantize_weight, residual_norm_quant, \
+    rope_inv_freq, row_quant
 from .kernels.activation import GELU_TANH
 from .kernels.attention import split_count
 
@@ -128,7 +132,7 @@ class Pi05Expert:
                                                     device=dev), A, k)
             self.xq, self.oq, self.hq = tiled(EX_D), tiled(HEADS * HEAD_DIM), tiled(EX_FF)
             self.layers = [ExpertLayer(pack_skinny(permute_rope_rows(L.qkv, HEADS, 1, HEAD_DIM)), pack_skinny(L.o),
-                                       pack_skinny(L.gate_up), pack_skinny(L.down)) for L in weights.layers]
+                                       pack_skinny(pack_glu(L.gate_up)), pack_skinny(L.down)) for L in weights.layers]
             splits = max(2, split_count(1, A, HEADS, 1, self.smax + A))
             self.split = SplitWorkspace(1, A, HEADS, 1, HEAD_DIM, splits, dev)
 
@@ -211,8 +215,8 @@ class Pi05Expert:
                 gemm(oq, L.o, raw(A, EX_D))
                 residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.o.scale,
                                     gate=ma[i, 2], mod_scale=mf[i, 0], mod_shift=mf[i, 1], q=xq, q_scale=s[0])
-                gemm(xq, L.gate_up, raw(A, 2 * EX_FF))
-                gated_act_quant(raw(A, 2 * EX_FF), hq, s[1], row=s[0], col=L.gate_up.scale, act=GELU_TANH)
+                linear(xq, s[0], L.gate_up, out=raw(A, EX_FF), act="geglu")
+                row_quant(raw(A, EX_FF), hq, s[1])
                 gemm(hq, L.down, raw(A, EX_D))
                 if i < last:
                     residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
