@@ -134,3 +134,42 @@ def test_fp8_linear_module_refuses_cpu_and_non_linear():
         Gfx950FP8Linear(torch.nn.Sequential(lin))
     with pytest.raises(ValueError, match="gfx950"):
         Gfx950FP8Linear(lin)  # CPU weights, no gfx950 target
+
+
+# ---------------------------------------------------------------------------
+# row order of linear_qkv_rope's weights (host side, no GPU)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("hd", [16, 64, 128, 256])
+def test_rope_row_order_pairs_rotary_partners_per_lane(hd):
+    # every head dim appears once, and each 4-row lane group of the skinny
+    # GEMM's output fragment holds (d, d + 1, d + hd/2, d + 1 + hd/2)
+    from instinctflash_amd.kernels.rope import _rope_row_order
+    order = _rope_row_order(hd)
+    assert sorted(order) == list(range(hd))
+    half = hd // 2
+    for p in range(0, hd, 4):
+        d = order[p]
+        assert d < half and d % 2 == 0
+        assert order[p:p + 4] == [d, d + 1, d + half, d + 1 + half]
+        # the decoding used by the kernel's epilogue: d = 8 * (p // 16) + 2 * ((p % 16) // 4)
+        assert d == 8 * (p // 16) + 2 * ((p % 16) // 4)
+
+
+def test_permute_rope_rows_on_cpu_tensors():
+    import torch
+    from instinctflash_amd.kernels.fp8 import Fp8Weight
+    from instinctflash_amd.kernels.rope import _rope_row_order, permute_rope_rows
+    hq, hkv, hd, K = 2, 1, 32, 16
+    N = (hq + 2 * hkv) * hd
+    w = torch.arange(N, dtype=torch.float32).repeat(K, 1).t().contiguous().to(torch.float8_e4m3fn)
+    scale = torch.arange(N, dtype=torch.float32)
+    bias = -torch.arange(N, dtype=torch.float32)
+    p = permute_rope_rows(Fp8Weight(w, scale, bias), hq, hkv, hd)
+    expect = [h * hd + o for h in range(hq + 2 * hkv) for o in _rope_row_order(hd)]
+    assert p.scale.tolist() == [float(i) for i in expect]
+    assert p.bias.tolist() == [-float(i) for i in expect]
+    assert torch.equal(p.w.view(torch.uint8), w.view(torch.uint8)[expect])
+    assert p.rope == (hq, hkv, hd)
+    with pytest.raises(ValueError):
+        permute_rope_rows(Fp8Weight(w, scale), hq, hkv + 1, hd)
