@@ -918,16 +918,18 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   p.nbw = glu ? 2 : 1;
   p.groups = N / (16 * p.nbw);
   const int64_t ksteps = (K + kBK - 1) / kBK;
-  // Split K in two when one token block meets at most 128 row groups (e.g. a
-  // 16 x 1536 x 6144 down projection: 96 groups would leave 160 CUs idle).
-  // Measured on MI355X: 9.4 -> 8.0 us there; more slices, or any split with
-  // several token blocks, lose more to the ticket and partial round trips
-  // (about 2-3 us of serial latency) than the extra CUs win.
+  // Split K in two for one token block, at most 128 row groups and a long K
+  // (>= 64 steps of 128): the two halves' chains run side by side. Measured
+  // on MI355X with weights streamed from HBM (tile layouts), split / not:
+  // 16x512x8192 6.3 / 6.9 us, 8x2048x8192 7.4 / 8.3, 1x1024x16384 9.2 / 11.3;
+  // at K = 3072..6144 the ticket and partial round trip costs more than it
+  // wins (16x1536x6144 6.3 / 6.2, 16x1024x4096 5.5 / 4.8). More slices, or
+  // any split with several token blocks, lose more.
   int64_t s = 1;
 #ifdef IFX_SK_SPLIT
   s = IFX_SK_SPLIT;
 #else
-  if (p.mb == 1 && p.groups <= kSkMaxGroups / 2 && ksteps >= 8) s = 2;
+  if (p.mb == 1 && p.groups <= kSkMaxGroups / 2 && ksteps >= 64) s = 2;
 #endif
   if (s < 1 || p.groups > kSkMaxGroups) s = 1;
   p.kss = (ksteps + s - 1) / s;

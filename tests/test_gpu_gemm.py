@@ -276,6 +276,13 @@ def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
     _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])
+def test_skinny_shorter_k_is_not_split(gpu, M, N, K):
+    # K < 64 steps: one workgroup per row group (the split's round trip costs more)
+    from instinctflash_amd import _lib
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, 0) == 0
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (200, 512, 1024), (1024, 2048, 2048)])
 def test_per_tensor_scales(gpu, oracle_mod, M, N, K):
     # per-tensor activation and weight scales (reference runtime/torch_fp8_linear.py:75-78)
@@ -321,11 +328,12 @@ def test_fp8_linear_module(gpu, oracle_mod):
         Gfx950FP8Linear(torch.nn.Linear(1000, 512, dtype=torch.bfloat16).to(gpu))
 
 
-@pytest.mark.parametrize("M,N,K,act", [(16, 1536, 6144, None), (1, 512, 1040, None), (9, 1024, 2064, "gelu_tanh"),
-                                       (16, 2048, 1536, "geglu"), (13, 4096, 16384, "swiglu")])
+@pytest.mark.parametrize("M,N,K,act", [(16, 1536, 8192, None), (1, 512, 8208, None), (9, 1024, 8336, "gelu_tanh"),
+                                       (16, 2048, 8192, "geglu"), (13, 4096, 16384, "swiglu")])
 def test_skinny_split_k(gpu, oracle_mod, M, N, K, act):
-    # one token block and <= 128 row groups: two workgroups per group split K and
-    # the last to arrive adds the partials (ticket counters in the workspace header)
+    # one token block, <= 128 row groups and K >= 64 steps of 128: two workgroups
+    # per group split K and the last to arrive adds the partials (ticket
+    # counters in the workspace header)
     from instinctflash_amd import _lib
     from instinctflash_amd.kernels import fp8 as F, pack_glu
     glu = act in ("geglu", "swiglu")
