@@ -1327,16 +1327,24 @@ inline bool big_path(int64_t M, int64_t K) { return M > 128 && K % kBigKB == 0; 
 //    per wave: the loop is latency-bound at these sizes), two workgroups per
 //    CU, usually no split (1024 x 2560 x 2048: 28 us with split-K narrow tiles,
 //    15.7 us with 2 waves of 64 x 64 and 64-byte stages, 12.1 us now);
+//  * kSmall32: as kSmall with 32-token tiles (2 waves of 64 x 32, four
+//    workgroups per CU) when 64-token tiles would give fewer than 256
+//    workgroups (200 x 2560 x 2048 10.7 -> 8.8 us, 512 x 1024 x 2048
+//    12.4 -> 10.6 us; at 256 or more the 64-token tiles win: 1024 x 2560 x 2048
+//    12.2 against 15.2 us);
 //  * kNarrow: fewer than 192 tiles and a longer K -- 128 tokens x 256 weight
 //    rows, 8 waves of 128 x 32, 128-byte stages, one workgroup per CU, plus
 //    split K (1024 x 2048 x 11008: 41 us; 44 us with 4 waves of 128 x 64 and
 //    64-byte stages, 67 us for small tiles without a split).
-enum class BigCfg { kWide, kWide192, kSmall, kNarrow };
+enum class BigCfg { kWide, kWide192, kSmall, kSmall32, kNarrow };
 
 inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
   const int64_t tm = (M + 255) / 256;
   const int64_t t256 = tm * ((N + 255) / 256);
-  if (t256 < 192) return K <= 4096 ? BigCfg::kSmall : BigCfg::kNarrow;
+  if (t256 < 192) {
+    if (K > 4096) return BigCfg::kNarrow;
+    return ((M + 63) / 64) * ((N + 127) / 128) < 256 ? BigCfg::kSmall32 : BigCfg::kSmall;
+  }
 #ifndef IFX_EXP_NO192
   if (!glu) {
     const int64_t t192 = tm * ((N + 191) / 192);
@@ -1359,6 +1367,8 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
       return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     case BigCfg::kSmall:
       return launch_big<64, 128, 128, 2, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+    case BigCfg::kSmall32:
+      return launch_big<32, 128, 128, 2, 4, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     default:
       return launch_big<128, 256, 128, 2, 1, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
@@ -1379,6 +1389,7 @@ size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilog
     case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
     case BigCfg::kWide: return big_plan(M, N, K, 256, 256, 128).ws_bytes;
     case BigCfg::kSmall: return big_plan(M, N, K, 64, 128, 128).ws_bytes;
+    case BigCfg::kSmall32: return big_plan(M, N, K, 32, 128, 128).ws_bytes;
     default: return big_plan(M, N, K, 128, 256, 128).ws_bytes;
   }
 }
