@@ -166,6 +166,25 @@ def test_ragged_small_grid_configs(gpu, oracle_mod, K, act, resgate):
            residual=r, gate=gt)
 
 
+@pytest.mark.parametrize("M,N,K,act", [(65, 256, 1040, None), (100, 768, 528, "gelu_tanh"), (300, 512, 1552, "geglu")])
+def test_unaligned_k_lds_path(gpu, oracle_mod, M, N, K, act):
+    # M > 64 with K % 128 != 0 runs the register-staged LDS kernel (everything
+    # else past the skinny range runs the large-M kernel)
+    from instinctflash_amd.kernels import pack_glu
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + K, bias=True)
+    res = torch.randn((M, N // 2 if act == "geglu" else N), generator=g).to(torch.bfloat16)
+    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if act == "geglu" else fw, f"lds {M}x{N}x{K}", ref_w=fw, act=act,
+           residual=res)
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 2048, 2048), (100, 2560, 2048), (128, 1024, 4096), (96, 1056, 8192)])
+def test_mid_m_large_kernel(gpu, oracle_mod, M, N, K):
+    # 64 < M <= 128 with K % 128 == 0: the large-M kernel's small-grid tiles
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N, bias=True)
+    res = torch.randn((M, N), generator=g).to(torch.bfloat16)
+    _check(gpu, oracle_mod, qa, sa, fw, f"mid {M}x{N}x{K}", residual=res)
+
+
 def test_fp32_output(gpu, oracle_mod):
     qa, sa, fw, _ = _make(gpu, 100, 512, 512, seed=8, bias=True)
     o32, _ = _check(gpu, oracle_mod, qa, sa, fw, "f32 out")
