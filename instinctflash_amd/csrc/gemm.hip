@@ -1482,6 +1482,11 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
   if (big_path(M, K))
     return glu ? launch_large<true>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
+  // Grids under one round of 256 x 128 tiles take 64 x 64 tiles (4 waves of
+  // 32 x 32): 100x2560x2064 35.5 -> 10.5 us, 1000x2048x2064 39.5 -> 16.8 us.
+  if (((M + 127) / 128) * ((N + 255) / 256) < 256)
+    return glu ? launch_lds<64, 64, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
+               : launch_lds<64, 64, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
   return glu ? launch_lds<256, 128, 2, 2, true>(A, lda, Wt, ldw, K, e, st)
              : launch_lds<256, 128, 2, 2, false>(A, lda, Wt, ldw, K, e, st);
 }

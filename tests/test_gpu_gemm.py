@@ -166,14 +166,17 @@ def test_ragged_small_grid_configs(gpu, oracle_mod, K, act, resgate):
            residual=r, gate=gt)
 
 
-@pytest.mark.parametrize("M,N,K,act", [(65, 256, 1040, None), (100, 768, 528, "gelu_tanh"), (300, 512, 1552, "geglu")])
+@pytest.mark.parametrize("M,N,K,act", [(65, 256, 1040, None), (100, 768, 528, "gelu_tanh"), (300, 512, 1552, "geglu"),
+                                       (1000, 2112, 1040, None), (2048, 8192, 272, "swiglu")])
 def test_unaligned_k_lds_path(gpu, oracle_mod, M, N, K, act):
     # M > 64 with K % 128 != 0 runs the register-staged LDS kernel (everything
-    # else past the skinny range runs the large-M kernel)
+    # else past the skinny range runs the large-M kernel): 64x64 tiles under one
+    # round of 256x128 tiles, 256x128 tiles above (2048x8192 GLU)
     from instinctflash_amd.kernels import pack_glu
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + K, bias=True)
-    res = torch.randn((M, N // 2 if act == "geglu" else N), generator=g).to(torch.bfloat16)
-    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if act == "geglu" else fw, f"lds {M}x{N}x{K}", ref_w=fw, act=act,
+    glu = act in ("geglu", "swiglu")
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if glu else fw, f"lds {M}x{N}x{K}", ref_w=fw, act=act,
            residual=res)
 
 
