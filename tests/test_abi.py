@@ -57,9 +57,11 @@ def test_workspace_queries(lib):
     # 816 x 2048 has 32 tiles: 1 KB counter header + fp32 split-K partials, whole M x N slices
     ws = lib.ifx_fp8_linear_workspace_size(816, 2048, 16384, 0)
     assert ws > 1024 and (ws - 1024) % (816 * 2048 * 4) == 0
-    # skinny: 96 row groups of the 16 x 1536 x 6144 down projection split K; header + partials
-    ws = lib.ifx_fp8_linear_workspace_size(16, 1536, 6144, 0)
+    # skinny: 96 row groups and K >= 64 steps of 128 split K; header + partials
+    ws = lib.ifx_fp8_linear_workspace_size(16, 1536, 8192, 0)
     assert ws > 1024 and (ws - 1024) % (96 * 64 * 16) == 0
+    # shorter K (the C2 down projection) runs unsplit
+    assert lib.ifx_fp8_linear_workspace_size(16, 1536, 6144, 0) == 0
     # quantize-and-project: the e4m3 copy + scales (+ per-tensor partials) + the GEMM's own
     assert lib.ifx_quant_linear_workspace_size(16, 6144, 1536, 0, _lib.SCALE_ROW) >= 16 * 1536 + 64
     assert (lib.ifx_quant_linear_workspace_size(64, 6144, 1536, 0, _lib.SCALE_TENSOR)
