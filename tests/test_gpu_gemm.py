@@ -180,12 +180,16 @@ def test_unaligned_k_lds_path(gpu, oracle_mod, M, N, K, act):
            residual=res)
 
 
-@pytest.mark.parametrize("M,N,K", [(65, 2048, 2048), (100, 2560, 2048), (128, 1024, 4096), (96, 1056, 8192)])
-def test_mid_m_large_kernel(gpu, oracle_mod, M, N, K):
+@pytest.mark.parametrize("M,N,K,act", [(65, 2048, 2048, None), (100, 2560, 2048, "gelu_tanh"), (128, 1024, 4096, None),
+                                       (96, 1056, 8192, None), (96, 4096, 1024, "geglu"), (72, 2048, 6144, "swiglu")])
+def test_mid_m_large_kernel(gpu, oracle_mod, M, N, K, act):
     # 64 < M <= 128 with K % 128 == 0: the large-M kernel's small-grid tiles
+    # (32-token tiles, split K for K > 4096), GLU included
+    from instinctflash_amd.kernels import pack_glu
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N, bias=True)
-    res = torch.randn((M, N), generator=g).to(torch.bfloat16)
-    _check(gpu, oracle_mod, qa, sa, fw, f"mid {M}x{N}x{K}", residual=res)
+    glu = act in ("geglu", "swiglu")
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if glu else fw, f"mid {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
 
 
 def test_fp32_output(gpu, oracle_mod):
