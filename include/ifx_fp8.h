@@ -182,8 +182,8 @@ int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const flo
  * sw: f32 [N] or NULL, bias: f32 [N] or NULL, gate: bf16 [N_out] or NULL.
  * workspace: at least ifx_fp8_linear_workspace_size(M,N,K,epilogue) bytes of
  * 16-byte aligned device memory, used when the GEMM splits K across
- * workgroups (too few output tiles, or for M <= 64 too few 16-row groups, to
- * fill the GPU); the size is 0 (NULL allowed) otherwise. Layout: a 1 KB header
+ * workgroups (too few output tiles, or for M <= 64 too few 16-row groups and a
+ * long K, to fill the GPU); the size is 0 (NULL allowed) otherwise. Layout: a 1 KB header
  * of per-group arrival counters, then fp32 partial sums. Zero-fill a workspace
  * once before its first use; every call leaves the header zeroed again, so one
  * workspace serves any sequence of calls and shapes. Calls that may overlap
