@@ -176,3 +176,16 @@ def test_contract_errors(gpu):
         attention(torch.zeros(1, 4, 1, 320, device=gpu, dtype=torch.bfloat16),
                   torch.zeros(1, 8, 1, 320, device=gpu, dtype=torch.bfloat16),
                   torch.zeros(1, 8, 1, 320, device=gpu, dtype=torch.bfloat16))  # D > 256
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_many_splits_long_keys(gpu, oracle_mod, dtype):
+    # 16 key splits over ~4000 keys: the partial rows are kept in the operands'
+    # 16-bit type (normalized by their own softmax sum); the merged output stays
+    # within the same bars as the unsplit kernel
+    from instinctflash_amd.kernels import SplitWorkspace, attention
+    q, k, v = _qkv(1, 33, 4000, 8, 1, 256, 21, dtype)
+    n = torch.tensor([3900], device=gpu, dtype=torch.int32)
+    ws = SplitWorkspace(1, 33, 8, 1, 256, 16, gpu)
+    out = attention(q.to(gpu), k.to(gpu), v.to(gpu), kv_len=n, split=ws)
+    _close(out, _ref(oracle_mod, q, k, v, np.full(33, 3900)), dtype, f"16 splits {dtype}")
