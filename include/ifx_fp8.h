@@ -390,8 +390,8 @@ int ifx_fp8_pack_glu(const void* w, const float* scale, const float* bias, int64
  * With kv_index (int32 [n_index]) key n is cache row kv_index[n].
  * o [B, Tq, Hq, D] (o_strides) = softmax(q k^T * scale) v per head.
  * splits > 1 spreads each row block's keys over `splits` workgroups, keeping
- * partial softmax states in `workspace` (ifx_attention_workspace_size bytes, no
- * zero-fill needed; partial rows normalized by their own softmax sum, in the
+ * partial softmax states in `workspace` (ifx_attention_workspace_size bytes,
+ * 16-byte aligned (else IFX_ERR_ALIGN), no zero-fill needed; partial rows normalized by their own softmax sum, in the
  * operands' 16-bit type), then merges them; o may then be NULL, and with q8 != NULL
  * (B == 1) every token's full output row [Hq * D] is also quantized per token to
  * e4m3 q8 [Tq, ldq8] with q8_scale [Tq] (this package's recipe, as

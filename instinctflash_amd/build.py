@@ -11,12 +11,14 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libifx_fp8.so"
+OBJ = PKG / "_build"
 SOURCES = ("quant.hip", "gemm.hip", "norm.hip", "rope.hip", "attention.hip")
 ARCH = "gfx950"
 
@@ -25,7 +27,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # IEEE round-to-nearest FP32 division is part of the quantization recipe.
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     # Keep FP32 denormals (bf16 subnormal inputs must quantize exactly).
@@ -46,15 +47,25 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 kernels cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    srcs = [str(CSRC / s) for s in SOURCES]
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, f"-I{ROOT / 'include'}", *srcs, "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile each source to an object (in parallel), then link the library."""
+    OBJ.mkdir(exist_ok=True)
+    objs = [OBJ / (Path(s).stem + ".o") for s in SOURCES]
+    cc = hipcc()
+    cmds = [[cc, *FLAGS, f"-I{ROOT / 'include'}", "-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

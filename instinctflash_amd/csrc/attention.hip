@@ -239,10 +239,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
 
   // Heads over 128 dims have no registers to spare for the next block's data:
   // they load each block right before staging it.
-#ifndef IFX_ATT_PREFETCH_MAX_DT
-#define IFX_ATT_PREFETCH_MAX_DT 4
-#endif
-  constexpr bool kPrefetch = DT <= IFX_ATT_PREFETCH_MAX_DT;
+  constexpr bool kPrefetch = DT <= 4;
   if (kPrefetch && start < end) fetch(start);
   for (int n0 = start; n0 < end; n0 += kBlockN) {
     if (!kPrefetch) fetch(n0);
@@ -260,11 +257,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lds + (32 * t + col) * kKPitch + 16 * c + 8 * half);
-#ifndef IFX_ATT_DBG_NO_QK
         s[t] = MF::run(kf, qf[c], s[t]);
-#else
-        s[t][0] += __uint_as_float(kf[0]);
-#endif
       }
     }
     // ---- online softmax (log2 domain); lane holds keys n0 + 32t + 8q + 4*half + r
@@ -334,11 +327,7 @@ __global__ __launch_bounds__(kAttnThreads, DT <= 4 ? 2 : 1) void attn_kernel(Att
           for (int dt = 0; dt < DT; ++dt) {
             const u32x2_t lo = lds_read_tr16(vbk + 32 * dt);
             const u32x2_t hi = lds_read_tr16(vbk + 8 * kVPitch + 32 * dt);
-#ifndef IFX_ATT_DBG_NO_PV
             acc[dt] = MF::run(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
-#else
-            acc[dt][0] += __uint_as_float(lo[0] ^ pf[0] ^ hi[1]);
-#endif
           }
         }
     }
@@ -572,6 +561,7 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
   if (splits == 1 && !o) return IFX_ERR_INVALID;
   if (splits > 1 && (!workspace || ws_bytes < ifx_attention_workspace_size(B, Tq, Hq, Hkv, D, splits)))
     return IFX_ERR_WORKSPACE;
+  if (splits > 1 && !aligned16(workspace)) return IFX_ERR_ALIGN;  // 16-byte partial-row stores
   if (o && !o_strides) return IFX_ERR_INVALID;
   if (B == 0 || Tq == 0) return IFX_OK;
   if (!q || !k || !v) return IFX_ERR_INVALID;

@@ -550,11 +550,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         const v8i wf = cat8(ld16(base + S::off(row, c0)), ld16(base + S::off(row, c0 + 1)));
 #pragma unroll
         for (int j = 0; j < kFM; ++j) {
-#ifdef IFX_DBG_READS_ONLY
-          acc[i][j][0] += __int_as_float((wf[0] ^ af[j][1]) & 0x3FFFFF) + __int_as_float((wf[7] ^ af[j][6]) & 0x3FFFFF);
-#else
           acc[i][j] = mfma32(wf, af[j], acc[i][j]);
-#endif
         }
       }
     }
@@ -570,25 +566,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-#ifndef IFX_DBG_NO_DMA
     if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-#endif
-#ifndef IFX_DBG_NO_MFMA
     compute(smem + (kt % STAGES) * kStage);
-#endif
   }
 
-#ifdef IFX_DBG_NO_EPI
-  {
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kFN; ++i)
-#pragma unroll
-      for (int j = 0; j < kFM; ++j) t += acc[i][j][0] + acc[i][j][7] + acc[i][j][15];
-    if (t == 1234.5f) static_cast<float*>(e.out)[tid] = t;
-    return;
-  }
-#endif
   if (part.base) {
     // Split-K: store this slice's raw accumulators; splitk_reduce applies the
     // epilogue. Through the same LDS transpose, 128 packed columns per row.
@@ -740,9 +721,6 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
               y[2] = res[tb].z + y[2];
               y[3] = res[tb].w + y[3];
             }
-#ifdef IFX_DBG_NO_STORE
-            if (y[0] == 1234.5f && y[1] == -1.f)
-#endif
             {
               if constexpr (kRt) {
                 epi_store4(e, mrow + t * kRowsPerPass, c_out, y);
@@ -820,9 +798,9 @@ __global__ __launch_bounds__(256) void splitk_reduce(Partials part, int ksplit, 
 // (nontemporal: read once per call) and token fragments before issuing their
 // MFMAs; partial sums are added in LDS in wave order.
 //
-// With ksplit > 1 each workgroup stores its fp32 partial with agent-scope
-// (cross-XCD coherent) stores, waits for them to complete and takes a ticket
-// on its group's counter; the workgroup that takes the last ticket adds the
+// With ksplit > 1 each workgroup stores its fp32 partial and takes a ticket
+// on its group's counter (an agent-scope release, so the partial is visible
+// device-wide first); the workgroup that takes the last ticket adds the
 // slices' partials in slice order (deterministic), resets the counter to zero
 // and runs the epilogue. No workgroup waits for another.
 
@@ -926,12 +904,7 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   // wins (16x1536x6144 6.3 / 6.2, 16x1024x4096 5.5 / 4.8). More slices, or
   // any split with several token blocks, lose more.
   int64_t s = 1;
-#ifdef IFX_SK_SPLIT
-  s = IFX_SK_SPLIT;
-#else
   if (p.mb == 1 && p.groups <= kSkMaxGroups / 2 && ksteps >= 64) s = 2;
-#endif
-  if (s < 1 || p.groups > kSkMaxGroups) s = 1;
   p.kss = (ksteps + s - 1) / s;
   p.ksplit = static_cast<int>((ksteps + p.kss - 1) / p.kss);
   // One token block per workgroup (grid.y over the blocks) when the row groups
@@ -964,18 +937,6 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
                    ? kWsHeader + static_cast<size_t>(p.ksplit) * p.groups * p.nbw * p.mb * 64 * 4 * sizeof(float)
                    : 0;
   return p;
-}
-
-__device__ __forceinline__ void store_agent4(float* p, const v4f v) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) __hip_atomic_store(p + r, v[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ v4f load_agent4(const float* p) {
-  v4f v;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = __hip_atomic_load(p + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
 }
 
 // TILED: w is in the layout of ifx_fp8_pack_skinny (2 KB tile per 16-row block
@@ -1057,9 +1018,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
       const bool hi = s < s_end && k0 + 16 < K;
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
-#ifdef IFX_DBG_SK_NO_W
-        wf[u][b] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
-#else
         if constexpr (TILED) {
           const bool in = s < s_end;
           const uint8_t* p = W + ((grp * NBW + b) * ksteps + s) * 2048 + lane * 16;
@@ -1068,14 +1026,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
           const uint8_t* p = wrow[b] + s * kBK;
           wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
         }
-#endif
       }
 #pragma unroll
       for (int j = 0; j < MB; ++j) {
         const uint8_t* p = arow[j] + s * kBK;
-#ifdef IFX_DBG_SK_NO_A
-        af[u][j] = v8i{(int)s, 1, 2, 3, 4, 5, 6, 7};
-#else
         if (a_tiled) {  // workgroup-uniform
           const bool in = s < s_end;
           const uint8_t* t = A + ((mb0 + j) * ksteps + s) * 2048 + lane * 16;
@@ -1083,7 +1037,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
         } else {
           af[u][j] = cat8(lo ? ld16(p) : v4i{0, 0, 0, 0}, hi ? ld16(p + 16) : v4i{0, 0, 0, 0});
         }
-#endif
       }
     }
 #pragma unroll
@@ -1117,24 +1070,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
     auto part = [&](int sl, int b) {
       return sp.part + ((((static_cast<int64_t>(sl) * groups + grp) * NBW + b) * MB + j) * 64 + lane) * 4;
     };
+    // Ordering (HIP memory model): every wave's partial stores precede the
+    // barrier; thread 0's ticket is an agent-scope acquire-release RMW, so its
+    // release makes all of them (cumulatively, through the barrier) visible
+    // device-wide before the count moves. The last arriver's RMW acquires every
+    // earlier slice's release; the barrier and each wave's agent-scope acquire
+    // fence extend that to all of its waves before they read the partials.
     if (wave < MB) {
 #pragma unroll
-      for (int b = 0; b < NBW; ++b) store_agent4(part(slice, b), sum[b]);
+      for (int b = 0; b < NBW; ++b) *reinterpret_cast<v4f*>(part(slice, b)) = sum[b];
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed before the ticket
     __syncthreads();
     if (tid == 0) {
-      const int t = __hip_atomic_fetch_add(sp.tickets + grp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int t = __hip_atomic_fetch_add(sp.tickets + grp, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       is_last = t == sp.ksplit - 1;
+      // reset for the next call (ordered after this kernel by the stream)
       if (is_last) __hip_atomic_store(sp.tickets + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!is_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (wave < MB) {
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
-        sum[b] = load_agent4(part(0, b));
-        for (int sl = 1; sl < sp.ksplit; ++sl) sum[b] += load_agent4(part(sl, b));
+        sum[b] = *reinterpret_cast<const v4f*>(part(0, b));
+        for (int sl = 1; sl < sp.ksplit; ++sl) sum[b] += *reinterpret_cast<const v4f*>(part(sl, b));
       }
     }
   }
@@ -1281,10 +1241,7 @@ int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint
   return launch_status();
 }
 
-#ifndef IFX_SKINNY_MAX_M
-#define IFX_SKINNY_MAX_M 64
-#endif
-constexpr int64_t kSkinnyMaxM = IFX_SKINNY_MAX_M;
+constexpr int64_t kSkinnyMaxM = 64;
 
 // One thread per 16-byte chunk of the tiled layout: chunk c = ((b * ks + s) *
 // 2 + half) * 64 + l holds row 16b + l%16, K bytes s*128 + 32*(l/16) + 16*half
@@ -1348,14 +1305,12 @@ inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
     if (K > 4096) return BigCfg::kNarrow;
     return ((M + 63) / 64) * ((N + 127) / 128) < 256 ? BigCfg::kSmall32 : BigCfg::kSmall;
   }
-#ifndef IFX_EXP_NO192
   if (!glu) {
     const int64_t t192 = tm * ((N + 191) / 192);
     // a 192-row tile does ~15% less work per unit time than a 256-row one
     // (measured: 8192x9216x3072, 6 full rounds of 192 vs 4.5 of 256, is 2.5% slower)
     if (((t192 + 255) / 256) * 192 * 115 < ((t256 + 255) / 256) * 256 * 100) return BigCfg::kWide192;
   }
-#endif
   return BigCfg::kWide;
 }
 

@@ -132,17 +132,28 @@ def _qout(name, q, M, K, device):
 
 
 _WORKSPACES: dict = {}
+_RETIRED: list = []
 
 
 def _workspace(nbytes: int, device, stream: int):
     """Workspace per (device, stream), reused by every call on that stream
     (calls on one stream are ordered). Zero-filled when allocated: its header
-    holds the split-K arrival counters, which every call leaves at zero."""
+    holds the split-K arrival counters, which every call leaves at zero.
+
+    A buffer outgrown by a later call is kept alive (never freed), because a
+    captured HIP graph may still hold its address. Growing while the stream is
+    being captured raises instead: run the captured calls once eagerly first,
+    so the buffer is already large enough."""
     if nbytes == 0:
         return None
     key = (device.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"the FP8 workspace of this stream must grow to {nbytes} bytes during HIP graph "
+                               "capture; run the captured calls once before capturing")
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws

@@ -66,6 +66,11 @@ class Call:
     kind: str      # "gemm" or "quant"
     work: object   # Gemm, or (M, K) of a quantizer pass
     fn: object     # fn(i): run with weight set i % pool
+    io: dict = field(default_factory=dict)
+    """The call's operands at weight set 0, for parity checks. quant: x (bf16
+    source), q (e4m3 rows or TiledRows), s (scales). gemm: a, sa, w (the weight
+    the kernel reads), w_ref (the same weight in the reference layout: gate
+    rows then up rows, not tiled), out, residual, gate, act."""
 
     @property
     def flops(self) -> int:
@@ -87,6 +92,7 @@ class Workload:
     pool: int = 1                   # rotating weight sets
     dominant: str = ""              # name of the kernel the roofline line reports
     tensors: dict = field(default_factory=dict)
+    ref: dict = field(default_factory=dict)  # weights in the reference layout, by projection
     _i: int = 0
 
     @property
@@ -139,11 +145,20 @@ def _act(g, M, K, outlier_frac=0.0, outlier_std=20.0):
     return x
 
 
-def _weights(g, N, K, dev, bias=False, glu=False):
+def _weights(g, N, K, dev, bias=False, glu=False, ref=None, name=None):
+    """Per-channel e4m3 weight N(0, 0.02) [+ bias N(0, 0.01)]; GLU weights are
+    repacked for the fused epilogue. With ``ref`` (a dict), the weight in the
+    reference layout is kept there under ``name`` for parity checks."""
     w = torch.randn((N, K), generator=g) * 0.02
     b = torch.randn(N, generator=g) * 0.01 if bias else None
     fw = F.quantize_weight(w, b, device=dev)
+    if ref is not None:
+        ref[name] = fw
     return F.pack_glu(fw) if glu else fw
+
+
+def _gemm_io(g: Gemm, a, sa, w, w_ref, out, residual=None, gate=None):
+    return dict(a=a, sa=sa, w=w, w_ref=w_ref, out=out, residual=residual, gate=gate, act=g.act)
 
 
 def _copies(fw, n):
@@ -178,7 +193,7 @@ class C1(Workload):
         self.pool = pool or _pool_size(N * K)
         # M <= 64 weights are packed once into the skinny tile layout; rotated
         # copies give identical numerics on distinct HBM lines.
-        ws = _copies(F.pack_skinny(_weights(g, N, K, dev, bias=True)), self.pool)
+        ws = _copies(F.pack_skinny(_weights(g, N, K, dev, bias=True, ref=self.ref, name="up")), self.pool)
         xb = x.to(torch.bfloat16).to(dev)
         self.tensors = dict(x=xb, w=ws, qa=F.quant_rows_tiled(xb),
                             out=torch.empty((M, N), dtype=torch.bfloat16, device=dev))
@@ -188,8 +203,10 @@ class C1(Workload):
         qa, sa = t["qa"]
         g = self.gemms[0]
         return [  # M <= 64: activations in the skinny tile layout
-            Call("quant x", "quant", (g.M, g.K), lambda i: F.quant_rows_tiled(t["x"], qa, sa)),
-            Call("up", "gemm", g, lambda i: F.linear(qa, sa, t["w"][i % self.pool], out=t["out"])),
+            Call("quant x", "quant", (g.M, g.K), lambda i: F.quant_rows_tiled(t["x"], qa, sa),
+                 dict(x=t["x"], q=qa, s=sa)),
+            Call("up", "gemm", g, lambda i: F.linear(qa, sa, t["w"][i % self.pool], out=t["out"]),
+                 _gemm_io(g, qa, sa, t["w"][0], self.ref["up"], t["out"])),
         ]
 
 
@@ -205,8 +222,8 @@ class C2(Workload):
                          [(M, D), (M, FF)], steps_per_unit=4, dominant="up")
         g = _gen(seed)
         xs = [_act(g, M, D) for _ in range(4)]  # fresh x per flow-matching step
-        w1 = _weights(g, FF, D, dev)
-        w2 = _weights(g, D, FF, dev)
+        w1 = _weights(g, FF, D, dev, ref=self.ref, name="up")
+        w2 = _weights(g, D, FF, dev, ref=self.ref, name="down")
         res = torch.randn((M, D), generator=g).to(torch.bfloat16)
         self.pool = pool or _pool_size(2 * FF * D)
         w1s = _copies(F.pack_skinny(w1), self.pool)
@@ -226,12 +243,16 @@ class C2(Workload):
         q2, s2 = t["q2"]
         up, down = self.gemms
         return [
-            Call("quant x", "quant", (up.M, up.K), lambda i: F.quant_rows_tiled(t["xs"][i % 4], q1, s1)),
+            Call("quant x", "quant", (up.M, up.K), lambda i: F.quant_rows_tiled(t["xs"][i % 4], q1, s1),
+                 dict(x=t["xs"][0], q=q1, s=s1)),
             Call("up", "gemm", up,
-                 lambda i: F.linear(q1, s1, t["w1"][i % self.pool], out=t["h"], act="gelu_tanh")),
-            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows_tiled(t["h"], q2, s2)),
+                 lambda i: F.linear(q1, s1, t["w1"][i % self.pool], out=t["h"], act="gelu_tanh"),
+                 _gemm_io(up, q1, s1, t["w1"][0], self.ref["up"], t["h"])),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows_tiled(t["h"], q2, s2),
+                 dict(x=t["h"], q=q2, s=s2)),
             Call("down", "gemm", down,
-                 lambda i: F.linear(q2, s2, t["w2"][i % self.pool], out=t["out"], residual=t["res"])),
+                 lambda i: F.linear(q2, s2, t["w2"][i % self.pool], out=t["out"], residual=t["res"]),
+                 _gemm_io(down, q2, s2, t["w2"][0], self.ref["down"], t["out"], residual=t["res"])),
         ]
 
 
@@ -248,8 +269,8 @@ class C3(Workload):
         g = _gen(seed)
         x = torch.randn((M, D), generator=g)
         x = x / x.pow(2).mean(dim=1, keepdim=True).sqrt()  # unit-RMS rows (post-RMSNorm)
-        wgu = _weights(g, 2 * FF, D, dev, glu=True)
-        wd = _weights(g, D, FF, dev)
+        wgu = _weights(g, 2 * FF, D, dev, glu=True, ref=self.ref, name="gate_up")
+        wd = _weights(g, D, FF, dev, ref=self.ref, name="down")
         res = torch.randn((M, D), generator=g).to(torch.bfloat16)
         b = _Buffers(dev)
         self.tensors = dict(x=x.to(torch.bfloat16).to(dev), wgu=wgu, wd=wd, res=res.to(dev), q1=b.q(M, D),
@@ -262,10 +283,14 @@ class C3(Workload):
         q2, s2 = t["q2"]
         gu, down = self.gemms
         return [
-            Call("quant x", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["x"], q1, s1)),
-            Call("gate_up", "gemm", gu, lambda i: F.linear(q1, s1, t["wgu"], out=t["h"], act="geglu")),
-            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], q2, s2)),
-            Call("down", "gemm", down, lambda i: F.linear(q2, s2, t["wd"], out=t["out"], residual=t["res"])),
+            Call("quant x", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["x"], q1, s1),
+                 dict(x=t["x"], q=q1, s=s1)),
+            Call("gate_up", "gemm", gu, lambda i: F.linear(q1, s1, t["wgu"], out=t["h"], act="geglu"),
+                 _gemm_io(gu, q1, s1, t["wgu"], self.ref["gate_up"], t["h"])),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], q2, s2),
+                 dict(x=t["h"], q=q2, s=s2)),
+            Call("down", "gemm", down, lambda i: F.linear(q2, s2, t["wd"], out=t["out"], residual=t["res"]),
+                 _gemm_io(down, q2, s2, t["wd"], self.ref["down"], t["out"], residual=t["res"])),
         ]
 
 
@@ -292,10 +317,10 @@ class C4(Workload):
         x_attn_in = _channel_outliers(g, M, D)
         x_o_in = _channel_outliers(g, M, D)
         x_mlp_in = _channel_outliers(g, M, D)
-        wqkv = _weights(g, qkv_n, D, dev, bias=True)
-        wo = _weights(g, D, D, dev)
-        wgu = _weights(g, 2 * FF, D, dev, glu=True)
-        wd = _weights(g, D, FF, dev)
+        wqkv = _weights(g, qkv_n, D, dev, bias=True, ref=self.ref, name="qkv")
+        wo = _weights(g, D, D, dev, ref=self.ref, name="o")
+        wgu = _weights(g, 2 * FF, D, dev, glu=True, ref=self.ref, name="gate_up")
+        wd = _weights(g, D, FF, dev, ref=self.ref, name="down")
         res = torch.randn((M, D), generator=g).to(torch.bfloat16)
         b = _Buffers(dev)
         bf = lambda t: t.to(torch.bfloat16).to(dev)  # noqa: E731
@@ -312,14 +337,22 @@ class C4(Workload):
         qh, sh = t["qh"]
         qkv, o, gu, down = self.gemms
         return [
-            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s)),
-            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"])),
-            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s)),
-            Call("o", "gemm", o, lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"])),
-            Call("quant mlp in", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["xm"], q, s)),
-            Call("gate_up", "gemm", gu, lambda i: F.linear(q, s, t["wgu"], out=t["h"], act="swiglu")),
-            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh)),
-            Call("down", "gemm", down, lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"])),
+            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s),
+                 dict(x=t["xa"], q=q, s=s)),
+            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"]),
+                 _gemm_io(qkv, q, s, t["wqkv"], self.ref["qkv"], t["qkv"])),
+            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s),
+                 dict(x=t["xo"], q=q, s=s)),
+            Call("o", "gemm", o, lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"]),
+                 _gemm_io(o, q, s, t["wo"], self.ref["o"], t["r1"], residual=t["res"])),
+            Call("quant mlp in", "quant", (gu.M, gu.K), lambda i: F.quant_rows(t["xm"], q, s),
+                 dict(x=t["xm"], q=q, s=s)),
+            Call("gate_up", "gemm", gu, lambda i: F.linear(q, s, t["wgu"], out=t["h"], act="swiglu"),
+                 _gemm_io(gu, q, s, t["wgu"], self.ref["gate_up"], t["h"])),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh),
+                 dict(x=t["h"], q=qh, s=sh)),
+            Call("down", "gemm", down, lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"]),
+                 _gemm_io(down, qh, sh, t["wd"], self.ref["down"], t["r2"], residual=t["r1"])),
         ]
 
 
@@ -339,10 +372,10 @@ class C5(Workload):
         xa = torch.randn((M, D), generator=g) * mod
         xo = torch.randn((M, D), generator=g) * mod
         xm = torch.randn((M, D), generator=g) * mod
-        wqkv = _weights(g, 3 * D, D, dev)
-        wo = _weights(g, D, D, dev)
-        wu = _weights(g, FF, D, dev)
-        wd = _weights(g, D, FF, dev)
+        wqkv = _weights(g, 3 * D, D, dev, ref=self.ref, name="qkv")
+        wo = _weights(g, D, D, dev, ref=self.ref, name="o")
+        wu = _weights(g, FF, D, dev, ref=self.ref, name="up")
+        wd = _weights(g, D, FF, dev, ref=self.ref, name="down")
         res = torch.randn((M, D), generator=g).to(torch.bfloat16)
         gate_o = torch.rand(D, generator=g).to(torch.bfloat16)
         gate_f = torch.rand(D, generator=g).to(torch.bfloat16)
@@ -361,16 +394,25 @@ class C5(Workload):
         qh, sh = t["qh"]
         qkv, o, up, down = self.gemms
         return [
-            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s)),
-            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"])),
-            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s)),
+            Call("quant attn in", "quant", (qkv.M, qkv.K), lambda i: F.quant_rows(t["xa"], q, s),
+                 dict(x=t["xa"], q=q, s=s)),
+            Call("qkv", "gemm", qkv, lambda i: F.linear(q, s, t["wqkv"], out=t["qkv"]),
+                 _gemm_io(qkv, q, s, t["wqkv"], self.ref["qkv"], t["qkv"])),
+            Call("quant o in", "quant", (o.M, o.K), lambda i: F.quant_rows(t["xo"], q, s),
+                 dict(x=t["xo"], q=q, s=s)),
             Call("o", "gemm", o,
-                 lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"], gate=t["gate_o"])),
-            Call("quant mlp in", "quant", (up.M, up.K), lambda i: F.quant_rows(t["xm"], q, s)),
-            Call("up", "gemm", up, lambda i: F.linear(q, s, t["wu"], out=t["h"], act="gelu_tanh")),
-            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh)),
+                 lambda i: F.linear(q, s, t["wo"], out=t["r1"], residual=t["res"], gate=t["gate_o"]),
+                 _gemm_io(o, q, s, t["wo"], self.ref["o"], t["r1"], residual=t["res"], gate=t["gate_o"])),
+            Call("quant mlp in", "quant", (up.M, up.K), lambda i: F.quant_rows(t["xm"], q, s),
+                 dict(x=t["xm"], q=q, s=s)),
+            Call("up", "gemm", up, lambda i: F.linear(q, s, t["wu"], out=t["h"], act="gelu_tanh"),
+                 _gemm_io(up, q, s, t["wu"], self.ref["up"], t["h"])),
+            Call("quant h", "quant", (down.M, down.K), lambda i: F.quant_rows(t["h"], qh, sh),
+                 dict(x=t["h"], q=qh, s=sh)),
             Call("down", "gemm", down,
-                 lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"], gate=t["gate_f"])),
+                 lambda i: F.linear(qh, sh, t["wd"], out=t["r2"], residual=t["r1"], gate=t["gate_f"]),
+                 _gemm_io(down, qh, sh, t["wd"], self.ref["down"], t["r2"], residual=t["r1"],
+                          gate=t["gate_f"])),
         ]
 
 
