@@ -5,7 +5,8 @@
  * argument is a DEVICE pointer except where noted; `stream` is a hipStream_t
  * (NULL = the null stream). No entry point allocates memory, synchronises the
  * host, or keeps mutable global state: the caller owns every buffer, so a call
- * may be captured into a HIP graph. Calls on distinct streams are independent,
+ * may be captured into a HIP graph. (The one exception, ifx_quant_linear_noalloc,
+ * works in a fixed scratch array that the library holds per GPU.) Calls on distinct streams are independent,
  * except that a workspace buffer must not be shared by calls that may overlap.
  *
  * Return value: IFX_OK (0), a negative IFX_ERR_* for an argument the library
@@ -42,6 +43,7 @@ extern "C" {
 #define IFX_ERR_ALIGN (-2)       /* a pointer/stride breaks 16-byte alignment    */
 #define IFX_ERR_WORKSPACE (-3)   /* workspace missing or smaller than required   */
 #define IFX_ERR_UNSUPPORTED (-4) /* shape not supported by any kernel variant    */
+#define IFX_ERR_SCRATCH (-5)     /* needs more than the library's fixed scratch  */
 
 /* source dtypes for the quantizers */
 #define IFX_DTYPE_BF16 0
@@ -406,6 +408,27 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
                   const int32_t* kv_len_dev, const int32_t* kv_extra, int causal, int64_t causal_offset,
                   const int32_t* kv_index, int64_t n_index, float scale, int splits, void* workspace,
                   size_t ws_bytes, void* q8, int64_t ldq8, float* q8_scale, void* stream);
+
+/*
+ * ifx_quant_linear without a workspace argument: the same two launches (plus a
+ * one-workgroup clear of the split-K ticket header), bit-identical output, but
+ * the workspace is a fixed scratch array inside the library
+ * (ifx_quant_linear_noalloc_max_bytes() = 64 MiB per GPU, held from the first
+ * call on that GPU until the process ends). No allocation of any kind.
+ * Rejects with IFX_ERR_SCRATCH a call whose ifx_quant_linear_workspace_size
+ * exceeds the scratch (about M * K bytes of e4m3 plus the split-K partials).
+ * The scratch is looked up on the CURRENT device (hipGetDevice), which must be
+ * the device of `stream` and of every operand. All calls on one GPU share its
+ * scratch: calls that may overlap on one GPU (distinct streams without
+ * ordering) race and must not be issued. a_scale as for ifx_quant_linear.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, serving loops and harnesses that forbid hipMalloc).
+ */
+size_t ifx_quant_linear_noalloc_max_bytes(void);
+int ifx_quant_linear_noalloc(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw,
+                             const float* sw, const float* bias, const void* residual, int64_t ldr,
+                             const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
+                             int64_t K, float* a_scale, void* stream);
 
 #ifdef __cplusplus
 }

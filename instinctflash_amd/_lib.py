@@ -22,6 +22,7 @@ ERR_INVALID = -1
 ERR_ALIGN = -2
 ERR_WORKSPACE = -3
 ERR_UNSUPPORTED = -4
+ERR_SCRATCH = -5
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
@@ -89,6 +90,9 @@ SIGNATURES = {
     "ifx_moe_act_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "ifx_quant_linear": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64, _I64,
                                 _P, _P, _SZ, _P]),
+    "ifx_quant_linear_noalloc_max_bytes": (_SZ, []),
+    "ifx_quant_linear_noalloc": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64,
+                                        _I64, _P, _P]),
     "ifx_fp8_linear": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64,
                               _I64, _I64, _P, _SZ, _P]),
     "ifx_fp8_pack_glu": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P]),

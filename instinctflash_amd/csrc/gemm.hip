@@ -36,6 +36,7 @@
 //    by the last workgroup to arrive (deterministic, no waiting).
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "ifx_abi.h"
@@ -1533,6 +1534,93 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
   const int flags = epilogue | (scale_mode == IFX_SCALE_TENSOR ? IFX_EPI_SCALAR_SA : 0);
   return ifx_fp8_linear(q, K, sa, w, ldw, sw, bias, residual, ldr, gate, flags, out, ldo, M, N, K, gws, ql.gemm,
                         stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// ifx_quant_linear_noalloc: ifx_quant_linear on a library-owned scratch buffer
+// ---------------------------------------------------------------------------
+//
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops that forbid hipMalloc). The workspace of ifx_quant_linear (split-K
+// tickets and partials, the e4m3 copy of x, the scales) lives in `scratch`, a
+// file-scope device array: every GPU the library runs on holds its own copy
+// (at its own address) until the process ends. Host code never passes the
+// array's name to a kernel (in host code it names a host-side shadow); it uses
+// the device address that hipGetSymbolAddress returns, looked up once per
+// device with that device current.
+
+namespace {
+
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of this device's `scratch`, or nullptr (status in *rc).
+void* scratch_ptr(int* rc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = IFX_ERR_UNSUPPORTED;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = e != hipSuccess ? static_cast<int>(e) : IFX_ERR_UNSUPPORTED;
+      return nullptr;
+    }
+    g_scratch[dev] = p;
+  }
+  *rc = IFX_OK;
+  return g_scratch[dev];
+}
+
+// Zeroes n 32-bit words (the split-K ticket header); a kernel rather than
+// hipMemsetAsync so the call stays graph-capturable without memset nodes.
+__global__ __launch_bounds__(256) void zero_words(int* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ifx_quant_linear_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int ifx_quant_linear_noalloc(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw,
+                             const float* sw, const float* bias, const void* residual, int64_t ldr,
+                             const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
+                             int64_t K, float* a_scale, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return IFX_ERR_INVALID;
+  if (M == 0)  // nothing to launch; let ifx_quant_linear validate the rest
+    return ifx_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N,
+                            K, a_scale, nullptr, 0, stream);
+  if (scale_mode != IFX_SCALE_ROW && scale_mode != IFX_SCALE_TENSOR) return IFX_ERR_INVALID;
+  const size_t need = ql_workspace(M, N, K, epilogue, scale_mode).total;
+  if (need > kScratchBytes) return IFX_ERR_SCRATCH;
+  int rc = IFX_OK;
+  void* ws = scratch_ptr(&rc);
+  if (!ws) return rc;
+  // The ticket header must read zero. Every call leaves it so, but a call that
+  // was rejected or interrupted mid-way need not have; clear it each time.
+  hipLaunchKernelGGL(zero_words, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<int*>(ws),
+                     static_cast<int>(kWsHeader / sizeof(int)));
+  rc = launch_status();
+  if (rc != IFX_OK) return rc;
+  return ifx_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K,
+                          a_scale, ws, kScratchBytes, stream);
 }
 
 }  // extern "C"

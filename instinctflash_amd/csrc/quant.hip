@@ -521,6 +521,7 @@ const char* ifx_status_string(int status) {
     case IFX_ERR_ALIGN: return "pointer or stride breaks 16-byte alignment";
     case IFX_ERR_WORKSPACE: return "workspace missing or too small";
     case IFX_ERR_UNSUPPORTED: return "shape not supported by any kernel variant";
+    case IFX_ERR_SCRATCH: return "call needs more than the library's fixed scratch buffer";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
   }
 }
