@@ -1,14 +1,15 @@
 #!/usr/bin/env python3
 """Benchmark of the FP8 projection path on one MI355X.
 
-    python bench.py [--config C2] [--steps K] [--warmup W] [--no-cpu] [--no-others]
+    python bench.py [--config C5] [--steps K] [--warmup W] [--no-cpu] [--no-others]
 
 A "step" is one pass of the hot path over one batch of synthetic input:
 per-token quantization of every projection input, the FP8 GEMMs with fused
 epilogues, and the re-quantization of GELU/GLU outputs. The headline workload is
-BASELINE configs[1] (C2: GR00T-style DiT action head, M=16, 4 flow-matching
-steps per timed unit), reported in GB/s of algorithmic HBM traffic; C1, C3, C4
-and C5 are measured in the same run and reported under "configs".
+the largest single-GPU configuration, C5 (Wan DiT block projections, M=8192),
+reported in TFLOP/s of FP8 GEMM work; C1-C4 are measured in the same run and
+reported under "configs", each with its own roofline and CPU baseline (C1/C2 in
+GB/s of algorithmic HBM traffic: they are bandwidth-bound).
 
 Timing: K steps are captured into one HIP graph (inputs already resident in HBM,
 weights rotating through a pool larger than the 256 MB Infinity Cache for
@@ -17,8 +18,13 @@ The dominant kernel's average duration is measured separately with HIP events
 around a graph of back-to-back launches of that kernel alone, on the stream it
 runs on, and gives the "roofline" object.
 
+The shader clock under the headline's dominant kernel is measured live: a
+one-wave probe kernel (ifx_sclk_probe) on a second stream counts shader cycles
+against the constant-rate wall clock while that kernel's graph replays.
+
 The CPU baseline runs the reference's PyTorch CPU FP8 path (oracle/cpu_path.py)
-on the host cores: whole C2 units, repeated until about 10 s of CPU time.
+on the host cores for every config: C1 and C2 whole, C3-C5 on a row sample
+(the same calls with fewer tokens), extrapolated linearly in M and labelled so.
 """
 from __future__ import annotations
 
@@ -99,6 +105,8 @@ def measure_calls(wl, launches):
     side = torch.cuda.Stream()
     for c in wl.calls():
         side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # eager first call on the capture stream (its workspace)
+            c.fn(0)
         g = capture(lambda i: c.fn(i), launches, side)
         time_graph(g)
         us = sorted(time_graph(g)[0] / launches * 1e3 for _ in range(5))[2]
@@ -137,6 +145,33 @@ def summarize(wl, m):
     res["frac_step"] = round(res["gbs"] / HBM_PEAK_GBS, 4) if wl.bound == "hbm" else \
         round(res["tflops"] / FP8_PEAK_TFLOPS, 4)
     return res
+
+
+def roofline(wl, m):
+    """Roofline object of the config's dominant kernel: algorithmic FLOPs (MFMA-
+    bound configs) or bytes (HBM-bound) per launch / its mean launch time (HIP
+    events around a graph of back-to-back launches on its own stream), against
+    the MI355X peak; `traffic` = calibrated HBM bytes per launch from the
+    committed profiles/hbm_traffic_<config>.md counter summary, when present."""
+    d = wl.dominant_gemm
+    k_s = m["kernel_ms"] * 1e-3
+    if wl.bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(d.bytes / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        roof = {"bound": "mfma", "achieved": round(d.flops / k_s / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
+                "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = None
+    measured = measured_traffic(wl.key)
+    if measured is not None:
+        roof["traffic"] = measured[0]
+        roof["traffic_source"] = measured[1]
+        roof["traffic_vs_algorithmic"] = round(measured[0] / d.bytes, 3)
+    roof["algorithmic_bytes"] = d.bytes
+    roof["algorithmic_flops"] = d.flops
+    roof["kernel"] = f"{d.name} {d.M}x{d.N}x{d.K}" + (f" {d.act}" if d.act else "")
+    roof["kernel_us"] = round(m["kernel_ms"] * 1e3, 3)
+    return roof
 
 
 def measure_producers(dev, launches=32):
@@ -219,50 +254,115 @@ def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     print(json.dumps({"probe": wl.key, "dominant": wl.dominant, "launches": launches, "copy_bytes": copy_bytes}))
 
 
-def cpu_baseline(min_seconds=10.0):
-    """Reference CPU FP8 path for one C2 unit (4 flow steps = 8 projections)."""
+def cpu_baseline(wl, max_rows=None, min_seconds=3.0):
+    """The reference's CPU FP8 path (oracle/cpu_path.py: per-token quant,
+    torch._scaled_mm via oneDNN, fp32 epilogue) over the config's calls, in its
+    order, on a bounded sample: min(M, max_rows) tokens, fewer if one step of
+    that would exceed ~min_seconds on this host (a 16-token step is timed
+    first to decide). Whole steps are repeated until ~min_seconds of CPU time;
+    with fewer than M tokens the time per step is extrapolated linearly to M
+    (labelled). Value in the config's unit (GB/s for HBM-bound configs, TFLOP/s
+    otherwise). A second line times the same step with dequantize-then-fp32-
+    matmul (MKL), the oracle's formulation."""
     import torch
     from oracle import cpu_path
-    from instinctflash_amd.workloads import C2, Gemm, quant_bytes
-    g = torch.Generator().manual_seed(0)
-    M, D, FF = 16, 1536, 6144
-    xs = [torch.randn((M, D), generator=g).to(torch.bfloat16) for _ in range(4)]
-    w1 = torch.randn((FF, D), generator=g) * 0.02
-    w2 = torch.randn((D, FF), generator=g) * 0.02
-    res = torch.randn((M, D), generator=g).to(torch.bfloat16)
-    q1, s1 = cpu_path.quant_rows(w1)
-    q2, s2 = cpu_path.quant_rows(w2)
-    cpu_path.c2_unit(xs, q1, s1, q2, s2, res)  # warm-up (oneDNN primitive creation)
-    units, t0 = 0, time.perf_counter()
-    while True:  # a bounded sample: whole units until ~min_seconds of CPU work
-        cpu_path.c2_unit(xs, q1, s1, q2, s2, res)
-        units += 1
-        dt = time.perf_counter() - t0
-        if dt >= min_seconds or units >= 100000:
-            break
-    dt /= units
-    gemms = [Gemm("up", M, FF, D, act="gelu_tanh"), Gemm("down", M, D, FF, residual=True)]
-    nbytes = 4 * (sum(x.bytes for x in gemms) + quant_bytes(M, D) + quant_bytes(M, FF))
-    # second line: the same unit with dequantize-then-fp32-matmul (MKL) in place of _scaled_mm
-    d1, d2 = q1.float() * s1[:, None], q2.float() * s2[:, None]
-    cpu_path.c2_unit_fp32(xs, d1, d2, res)
-    units32, t0 = 0, time.perf_counter()
-    while True:
-        cpu_path.c2_unit_fp32(xs, d1, d2, res)
-        units32 += 1
-        dt32 = time.perf_counter() - t0
-        if dt32 >= min_seconds / 2 or units32 >= 100000:
-            break
-    dt32 /= units32
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "dequant_fp32_matmul": {"value": round(nbytes / dt32 / 1e9, 4), "unit": "GB/s",
-                                    "seconds_per_unit": round(dt32, 6), "units_timed": units32,
-                                    "sample": "same C2 units: per-token quant, dequantize, fp32 matmul (MKL), "
-                                              "fp32 epilogue"},
-            "kind": "port", "seconds_per_unit": round(dt, 4), "units_timed": units,
-            "sample": f"{units} full C2 units (4 flow steps x [quant, 16x1536->6144 GELU, quant, 16x6144->1536 "
-                      "+res]) via torch._scaled_mm (oneDNN) on the host CPU, reference GI decomposition",
+    M = wl.gemms[0].M
+    gen = torch.Generator().manual_seed(0)
+    weights = []
+    for gm in wl.gemms:
+        w8, sw = cpu_path.quant_rows(torch.randn((gm.N, gm.K), generator=gen) * 0.02)
+        weights.append((gm, w8, sw, w8.float() * sw[:, None],
+                        torch.randn(gm.N, generator=gen) * 0.01 if gm.bias else None,
+                        torch.rand(gm.n_out, generator=gen).to(torch.bfloat16) if gm.gate else None))
+
+    def inputs(r):
+        return [(torch.randn((r, gm.K), generator=gen).to(torch.bfloat16),
+                 torch.randn((r, gm.n_out), generator=gen).to(torch.bfloat16) if gm.residual else None)
+                for gm, *_ in weights]
+
+    def step(xs, fp32):
+        for _ in range(wl.steps_per_unit):
+            for (gm, w8, sw, wd, bias, gate), (x, res) in zip(weights, xs):
+                q, sa = cpu_path.quant_rows(x)
+                if fp32:
+                    cpu_path.linear_fp32(q, sa, wd, bias=bias, act=gm.act, residual=res, gate=gate)
+                else:
+                    cpu_path.linear(q, sa, w8, sw, bias=bias, act=gm.act, residual=res, gate=gate)
+
+    def timed(xs, fp32, budget):
+        step(xs, fp32)  # warm-up (oneDNN primitive creation)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            step(xs, fp32)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget or n >= 100000:
+                return dt / n, n
+
+    r = M if max_rows is None else min(M, max_rows)
+    rc = min(r, 16)
+    t_cal, _ = timed(inputs(rc), False, 0.0)
+    if t_cal * r / rc > min_seconds:
+        r = max(rc, int(min_seconds / t_cal * rc) // 16 * 16)
+    xs = inputs(r)
+    t8, n8 = timed(xs, False, min_seconds)
+    t32, n32 = timed(xs, True, min_seconds / 2)
+    t8, t32 = t8 * M / r, t32 * M / r
+
+    def value(t):
+        return round(wl.bytes / t / 1e9, 4) if wl.bound == "hbm" else round(wl.flops / t / 1e12, 6)
+
+    unit = "GB/s" if wl.bound == "hbm" else "TFLOP/s"
+    what = f"{n8} whole steps of {wl.key}" if r == M else \
+        f"{n8} steps of {wl.key} on {r} of its {M} tokens, time extrapolated x{M / r:g} (linear in M)"
+    return {"value": value(t8), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "extrapolated": r != M, "seconds_per_step": round(t8, 6),
+            "sample": f"{what}: per-token quant, torch._scaled_mm (oneDNN), fp32 epilogue on the host CPU "
+                      "(reference GI decomposition)",
+            "dequant_fp32_matmul": {"value": value(t32), "unit": unit, "seconds_per_step": round(t32, 6),
+                                    "steps_timed": n32,
+                                    "sample": "same calls and tokens: per-token quant, dequantize, fp32 matmul "
+                                              "(MKL), fp32 epilogue"},
             "cpu": _cpu_model(), "os_cpu_count": os.cpu_count()}
+
+
+CPU_ROWS = {"C1": None, "C2": None, "C3": 256, "C4": 256, "C5": 256}
+
+
+def measure_sclk(wl, kernel_ms, wall_ms=20.0, launches=16):
+    """Shader clock (MHz) while the dominant kernel runs back to back, and idle:
+    ifx_sclk_probe on a second stream (default priority) spins `wall_ms` of the
+    wall clock while at least 3x that much dominant-kernel work is queued ahead
+    of it on the main stream."""
+    import ctypes
+
+    import torch
+    from instinctflash_amd import _lib
+    lib = _lib.load()
+    khz = ctypes.c_int(0)
+    _lib.check(lib.ifx_wall_clock_khz(ctypes.byref(khz)), "ifx_wall_clock_khz")
+    ticks = int(wall_ms * khz.value)
+    buf = torch.zeros(2, dtype=torch.int64, device="cuda")
+    main, side = torch.cuda.Stream(), torch.cuda.Stream()
+    main.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(main):  # eager first call on the capture stream (its workspace)
+        wl.dominant_call(0)
+    g = capture(lambda i: wl.dominant_call(i), launches, main)
+    reps = max(1, int(3 * wall_ms / (kernel_ms * launches)) + 1)
+    res = {}
+    for busy in (True, False):
+        torch.cuda.synchronize()
+        if busy:
+            for _ in range(reps):
+                g.replay()  # on `main`, the capture stream
+        _lib.check(lib.ifx_sclk_probe(buf.data_ptr(), ticks, side.cuda_stream), "ifx_sclk_probe")
+        torch.cuda.synchronize()
+        cyc, wt = (int(v) for v in buf.cpu())
+        res["busy" if busy else "idle"] = round(cyc / (wt / (khz.value * 1e3)) / 1e6, 1)
+    del g
+    return {"sclk_mhz_under_kernel": res["busy"], "sclk_mhz_idle": res["idle"], "wall_clock_khz": khz.value,
+            "method": f"ifx_sclk_probe ({wall_ms:g} ms of wall clock) on a second stream while "
+                      f"{reps * launches} back-to-back launches of the dominant kernel run; idle: the probe alone"}
 
 
 def measured_traffic(config):
@@ -290,7 +390,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--config", default="C5", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true")
     ap.add_argument("--probe", action="store_true",
@@ -316,7 +416,7 @@ def main():
         probe(CONFIGS[args.config](dev), dev)
         return
 
-    results = {}
+    results, metas = {}, {}
     order = [args.config] + ([] if args.no_others else [k for k in CONFIGS if k != args.config])
     for key in order:
         wl = CONFIGS[key](dev)
@@ -325,51 +425,41 @@ def main():
         m = measure(wl, steps, args.warmup)
         results[key] = summarize(wl, m)
         results[key]["steps"] = steps
+        results[key]["roofline"] = roofline(wl, m)
         results[key]["calls"] = measure_calls(wl, 32 if wl.bound == "hbm" else 8)
         if key == args.config:
-            head = (wl, m)
+            head_m = m
+            results[key]["roofline"].update(measure_sclk(wl, m["kernel_ms"]))
+            sclk = results[key]["roofline"]["sclk_mhz_under_kernel"]
+            if wl.bound == "mfma" and sclk > 0:
+                # dense FP8 peak at the measured clock: 256 CUs x 8192 FLOP/clk
+                at = 256 * 8192 * sclk * 1e6 / 1e12
+                results[key]["roofline"]["peak_at_sclk"] = round(at, 1)
+                results[key]["roofline"]["frac_at_sclk"] = round(results[key]["roofline"]["achieved"] / at, 4)
+        wl.tensors, wl.ref = {}, {}  # keep the shapes (CPU baseline), free the device tensors
+        metas[key] = wl
         del wl
         torch.cuda.empty_cache()
 
-    wl, m = head
-    r = results[args.config]
-    d = wl.dominant_gemm
-    k_s = m["kernel_ms"] * 1e-3
-    if wl.bound == "hbm":
-        value, unit = r["gbs"], "GB/s"
-        roof = {"bound": "hbm", "achieved": round(d.bytes / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s"}
-    else:
-        value, unit = r["tflops"], "TFLOP/s"
-        roof = {"bound": "mfma", "achieved": round(d.flops / k_s / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
-                "unit": "TFLOP/s"}
-    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
-    measured = measured_traffic(args.config)
-    if measured is not None:
-        # HBM bytes per launch of the dominant kernel from calibrated FETCH_SIZE /
-        # WRITE_SIZE counter runs (summary and commands in the profiles/ file)
-        roof["traffic"] = measured[0]
-        roof["traffic_source"] = measured[1]
-        roof["traffic_vs_algorithmic"] = round(measured[0] / d.bytes, 3)
-    roof["algorithmic_bytes"] = d.bytes
-    roof["kernel"] = r["dominant"]["kernel"]
-    roof["kernel_us"] = r["dominant"]["us"]
-
+    wl, m, r = metas[args.config], head_m, results[args.config]
+    value, unit = (r["gbs"], "GB/s") if wl.bound == "hbm" else (r["tflops"], "TFLOP/s")
     out = {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(m["step_ms"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 x fp8-e4m3 -> fp32 acc, bf16 out",
         "data": "synthetic (seeded torch.Generator on CPU, random-init weights quantized per channel)",
-        "config": {"workload": f"{args.config}: {wl.title}", "M": d.M, "gpu": arch,
+        "config": {"workload": f"{args.config}: {wl.title}", "M": wl.gemms[0].M, "gpu": arch,
                    "timed_unit": "4 flow-matching steps" if wl.steps_per_unit > 1 else "one pass"},
-        "roofline": roof,
+        "roofline": r["roofline"],
     }
     if not args.no_others:
         out["producers"] = measure_producers(dev)
         out["engine"] = measure_engine(dev)
     if not args.no_cpu:
-        _log("[bench] CPU baseline (reference CPU FP8 path, one C2 unit)")
-        out["cpu_baseline"] = cpu_baseline()
+        for key in order:
+            _log(f"[bench] CPU baseline {key} (reference CPU FP8 path)")
+            results[key]["cpu_baseline"] = cpu_baseline(metas[key], CPU_ROWS[key])
+        out["cpu_baseline"] = results[args.config]["cpu_baseline"]
     out["configs"] = results
     print(json.dumps(out))
 

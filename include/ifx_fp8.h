@@ -430,6 +430,17 @@ int ifx_quant_linear_noalloc(const void* x, int64_t ldx, int scale_mode, const v
                              const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                              int64_t K, float* a_scale, void* stream);
 
+/*
+ * Measurement helpers (no counterpart in the reference; used by bench.py to
+ * record the shader clock under load). ifx_sclk_probe launches one wave that
+ * spins for `wall_ticks` ticks of the constant-rate wall clock and writes
+ * out[0] = shader-clock cycles elapsed, out[1] = wall-clock ticks elapsed
+ * (uint64 [2], device, 16-byte aligned). ifx_wall_clock_khz reports the wall
+ * clock's rate (host int) for the current device.
+ */
+int ifx_sclk_probe(void* out, int64_t wall_ticks, void* stream);
+int ifx_wall_clock_khz(int* khz);
+
 #ifdef __cplusplus
 }
 #endif

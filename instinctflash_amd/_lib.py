@@ -93,6 +93,8 @@ SIGNATURES = {
     "ifx_quant_linear_noalloc_max_bytes": (_SZ, []),
     "ifx_quant_linear_noalloc": (_INT, [_P, _I64, _INT, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64, _I64,
                                         _I64, _P, _P]),
+    "ifx_sclk_probe": (_INT, [_P, _I64, _P]),
+    "ifx_wall_clock_khz": (_INT, [ctypes.POINTER(_INT)]),
     "ifx_fp8_linear": (_INT, [_P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _INT, _P, _I64, _I64,
                               _I64, _I64, _P, _SZ, _P]),
     "ifx_fp8_pack_glu": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P]),

@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libifx_fp8.so"
 OBJ = PKG / "_build"
-SOURCES = ("quant.hip", "gemm.hip", "norm.hip", "rope.hip", "attention.hip")
+SOURCES = ("quant.hip", "gemm.hip", "norm.hip", "rope.hip", "attention.hip", "clock.hip")
 ARCH = "gfx950"
 
 FLAGS = [

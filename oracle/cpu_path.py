@@ -28,9 +28,10 @@ def quant_rows(x: torch.Tensor):
     return q, scale
 
 
-def linear(q, sa, w8, sw, bias=None, act=None, residual=None, gate=None):
-    raw = torch._scaled_mm(q, w8.t(), scale_a=_ONE, scale_b=_ONE, out_dtype=torch.bfloat16)
-    y = raw.float() * sa[:, None] * sw[None, :]
+def _epilogue(y, bias=None, act=None, residual=None, gate=None):
+    """fp32 consumer math of the reference (kernels/norm.py:45-58,135-144,
+    kernels/activation.py:26-40): + bias, activation (GLU halves: gate rows
+    then up rows), * adaLN gate, + residual, then bf16."""
     if bias is not None:
         y = y + bias
     if act == "gelu_tanh":
@@ -46,6 +47,11 @@ def linear(q, sa, w8, sw, bias=None, act=None, residual=None, gate=None):
     return y.to(torch.bfloat16)
 
 
+def linear(q, sa, w8, sw, bias=None, act=None, residual=None, gate=None):
+    raw = torch._scaled_mm(q, w8.t(), scale_a=_ONE, scale_b=_ONE, out_dtype=torch.bfloat16)
+    return _epilogue(raw.float() * sa[:, None] * sw[None, :], bias, act, residual, gate)
+
+
 def c2_unit(xs, w1, s1, w2, s2, res):
     """One timed unit of config C2: 4 flow-matching steps of up(GELU) + down(+res)."""
     out = None
@@ -57,17 +63,10 @@ def c2_unit(xs, w1, s1, w2, s2, res):
     return out
 
 
-def linear_fp32(q, sa, wd, bias=None, act=None, residual=None):
+def linear_fp32(q, sa, wd, bias=None, act=None, residual=None, gate=None):
     """Dequantize-then-fp32-matmul (benchmarks/native/fp8_probe.py:36): wd is the
     dequantized weight (q_w * s_w) in fp32; the activation is dequantized per row."""
-    y = (q.float() * sa[:, None]) @ wd.t()
-    if bias is not None:
-        y = y + bias
-    if act == "gelu_tanh":
-        y = Fn.gelu(y, approximate="tanh")
-    if residual is not None:
-        y = residual.float() + y
-    return y.to(torch.bfloat16)
+    return _epilogue((q.float() * sa[:, None]) @ wd.t(), bias, act, residual, gate)
 
 
 def c2_unit_fp32(xs, wd1, wd2, res):
