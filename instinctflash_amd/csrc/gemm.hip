@@ -22,7 +22,7 @@
 // unchanged.
 //
 // Kernels (dispatch in ifx_fp8_linear)
-//  * gemm_big (M > 128, K % 128 == 0): 256 weight rows x 256 (or 128) tokens
+//  * gemm_big (M > 64, K % 128 == 0): 256 weight rows x 256 (or fewer) tokens
 //    per workgroup, 32x32x64 MFMAs, operands copied global -> LDS by
 //    direct-to-LDS DMA through a multi-stage ring, LDS-staged epilogue; split K
 //    (+ splitk_reduce) when the output has too few tiles to fill the GPU.
@@ -362,8 +362,11 @@ __global__ __launch_bounds__(WGN* WGM * 64, 1) void gemm_lds(const uint8_t* __re
 // Large-M kernel: direct-to-LDS multi-stage ring, 32x32x64 matrix cores
 // ---------------------------------------------------------------------------
 //
-// Workgroup tile: 256 weight rows x BM tokens, 2 x BM/64 waves (2 along weight
-// rows), wave tile 128 x 64, built from v_mfma_f32_32x32x64_f8f6f4 (the 32x32 form keeps
+// Workgroup tile: BN weight rows x BM tokens, 2 x BM/(32 FM) waves (2 along
+// weight rows), wave tile BN/2 x 32 FM: 128 x 64 with 8 waves (FM = 2), or
+// 128 x 128 with 4 waves (FM = 4: accumulators in AccVGPRs, a third less LDS
+// read traffic per MFMA, and a register-pipelined K loop, described at the
+// loop), built from v_mfma_f32_32x32x64_f8f6f4 (the 32x32 form keeps
 // the matrix pipe ~97% busy from a single wave per SIMD on gfx950; the 16x16x128
 // form reaches ~75% there). Operand roles as in the other kernels: weights are
 // source 0, so a lane of a 32x32 fragment holds, for q = 0..3, the four
@@ -507,6 +510,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   const int lrow = lane / S::kChunks;
   const int lpos = lane % S::kChunks;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(smem) + wave * kLoads * 1024);
+  const int64_t n_last = e.N - 1, m_last = e.M - 1;
   auto issue = [&](int kl) {  // local stage index kl: K stage kt0 + kl, ring slot kl % STAGES
     const int kt = kt0 + kl;
     const uint32_t buf = lds_base + (kl % STAGES) * kStage;
@@ -517,9 +521,9 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       const int64_t k0 = static_cast<int64_t>(kt) * KB + ((lpos ^ S::f(row)) << 4);
       const uint8_t* p;
       if (blk * kRowsPerDma < BN) {  // wave-uniform
-        p = W + min(n0 + row, e.N - 1) * ldw + k0;
+        p = W + min(n0 + row, n_last) * ldw + k0;
       } else {
-        p = A + min(m0 + (row - BN), e.M - 1) * lda + k0;
+        p = A + min(m0 + (row - BN), m_last) * lda + k0;
       }
       dma16(p, buf + i * 1024);
     }
@@ -557,18 +561,117 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
   };
 
+  if constexpr (FM == 4) {
+    // Register-pipelined 4-wave form (wave tile 128 x 128, accumulators in
+    // AccVGPRs). A 128-byte stage holds two 32x32x64 K steps (halves); the
+    // fragments of the next half are read from LDS into the other register
+    // set while the MFMAs of the current half run, so the matrix pipe does not
+    // wait on LDS latency. Per stage kt:
+    //   half 0: MFMAs on (kt, 0), reads of (kt, 1);
+    //   s_waitcnt lgkmcnt(0) (this wave is done reading slot kt) and vmcnt(0)
+    //   (its DMA of stage kt+1 landed); s_barrier (for every wave: stage kt+1
+    //   is in LDS and slot kt is free);
+    //   half 1: MFMAs on (kt, 1), reads of (kt+1, 0), and the DMA of stage
+    //   kt+2 into slot kt, one instruction after each MFMA.
+    static_assert(KB == 128 && STAGES == 2 && kFN == 4 && kFM == 4 && kLoads == 16, "4-wave 128 x 128 layout");
+    // this wave's DMA sources: one operand (wave-uniform base) and a 32-bit byte
+    // offset per lane, formed per instruction (row clamp + multiply-add) so that
+    // no address registers stay live; the launch guarantees both operands span
+    // < 4 GiB and rows * ld < 2^24 * 2^24. DMA i of a stage covers tile rows
+    // 8*(wave*16 + i) + lrow; its chunk swizzle depends only on i's parity.
+    static_assert(kRowsPerDma == 8, "128-byte rows");
+    const bool dw = wave * kLoads * kRowsPerDma < BN;
+    const uintptr_t dsel = reinterpret_cast<uintptr_t>(dw ? W : A);
+    const uint8_t* dbase = reinterpret_cast<const uint8_t*>(
+        static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(dsel)))) |
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(dsel >> 32))))
+         << 32));
+    const int drow0 = (dw ? static_cast<int>(n0) + wave * kLoads * 8 : static_cast<int>(m0) + wave * kLoads * 8 - BN) + lrow;
+    const int dlast = static_cast<int>(dw ? n_last : m_last);
+    const uint32_t dld = static_cast<uint32_t>(dw ? ldw : lda);
+    const uint32_t dkc0 = static_cast<uint32_t>(kt0) * KB + ((lpos ^ lrow) << 4);        // even i
+    const uint32_t dkc1 = static_cast<uint32_t>(kt0) * KB + ((lpos ^ lrow ^ 1) << 4);    // odd i
+    auto dma_one = [&](int kl, int i) {
+      const uint32_t row = static_cast<uint32_t>(min(drow0 + 8 * i, dlast));
+      const uint32_t off = __umul24(row, dld) + ((i & 1) ? dkc1 : dkc0) + static_cast<uint32_t>(kl) * KB;
+      dma16s(dbase, off, lds_base + (kl % STAGES) * kStage + i * 1024);
+    };
+    // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (8+2j, 9+2j)
+    v4i fr[2][16];
+    auto read_one = [&](const uint8_t* base, v4i* f, int h, int r) {
+      const int row = r < 2 * kFN ? wn * (32 * kFN) + (r >> 1) * 32 + frow : BN + wm * kWT + ((r - 2 * kFN) >> 1) * 32 + frow;
+      f[r] = ld16(base + S::off(row, 4 * h + 2 * fhalf + (r & 1)));
+    };
+    auto mfma_one = [&](const v4i* f, int m) {
+      const int i = m / kFM, j = m % kFM;
+      acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[8 + 2 * j], f[9 + 2 * j]), acc[i][j]);
+    };
+    auto interleave = [] {  // keep the MFMA / LDS-read alternation
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nk) issue(s);
-  for (int kt = 0; kt < nk; ++kt) {
-    // Loads of stages kt+1 .. kt+STAGES-2 may stay in flight.
-    if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();
-    else wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-    compute(smem + (kt % STAGES) * kStage);
+      for (int m = 0; m < 16; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    };
+    auto wait_lgkm0 = [] { __builtin_amdgcn_s_waitcnt(0xC07F); };  // lgkmcnt(0), visible to the compiler
+    auto sync = [&] {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    // prologue: stages 0 and 1 in flight, stage 0 landed, its half-0 fragments read
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) dma_one(0, i);
+    if (nk > 1) {
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) dma_one(1, i);
+      wait_vmcnt<kLoads>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) read_one(smem, fr[0], 0, r);
+    auto stage = [&](int kt, auto dma_tag) {
+      constexpr bool kDma = decltype(dma_tag)::value;  // stage kt + 2 exists
+      const uint8_t* cur = smem + (kt % STAGES) * kStage;
+      const uint8_t* nxt = smem + ((kt + 1) % STAGES) * kStage;  // after the last stage: a settled slot, unused
+      wait_lgkm0();
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        mfma_one(fr[0], m);
+        read_one(cur, fr[1], 1, m);
+      }
+      interleave();
+      wait_lgkm0();
+      if (kDma || kt + 1 < nk) wait_vmcnt<0>();
+      sync();
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        mfma_one(fr[1], m);
+        read_one(nxt, fr[0], 0, m);
+        if constexpr (kDma) dma_one(kt + 2, m);
+      }
+      interleave();
+    };
+    int kt = 0;
+    for (; kt + 2 < nk; ++kt) stage(kt, std::true_type{});
+    for (; kt < nk; ++kt) stage(kt, std::false_type{});
+    wait_vmcnt<0>();  // no DMA may still write LDS when the epilogue reuses it
+  } else {
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+      // Loads of stages kt+1 .. kt+STAGES-2 may stay in flight.
+      if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();
+      else wait_vmcnt<0>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+      compute(smem + (kt % STAGES) * kStage);
+    }
   }
 
   if (part.base) {
@@ -647,7 +750,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 
   // Mode bits: 1 GELU-tanh (GeGLU for GLU), 2 SiLU (SwiGLU), 4 gate,
   // 8 residual, 16 runtime flags (f32 residual or output, any combination).
-  auto rows = [&](auto mode_tag) {
+  auto rows = [&](auto mode_tag) __attribute__((always_inline)) {
     constexpr int MD = decltype(mode_tag)::value;
     constexpr bool kRt = (MD & 16) != 0;
     const int fl = e.flags;
@@ -667,9 +770,14 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       const int64_t left = e.M - (mw + j * 32);      // rows of this fragment row inside M
       // residual rows are loaded kResBatch at a time, ahead of their math
       constexpr int kResBatch = kRowIters < 8 ? kRowIters : 8;
-      if (col_ok) {
+      // A fragment row wholly inside M runs without per-row guards, so the
+      // compiler can interleave the rows' arithmetic.
+      auto emit = [&](auto full_tag) __attribute__((always_inline)) {
+        constexpr bool kFull = decltype(full_tag)::value;
         uint16_t* orow = static_cast<uint16_t*>(e.out) + mrow * e.ldo + c_out;
-#pragma unroll
+        // one batch of rows at a time keeps the accumulator-holding 4-wave
+        // kernel within its registers
+#pragma unroll 1
         for (int t0 = 0; t0 < kRowIters; t0 += kResBatch) {
         float4 res[kResBatch];
 #pragma unroll
@@ -677,7 +785,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
           const int t = t0 + tb;
           const int r = r0 + t * kRowsPerPass;
           if constexpr (kRt) {
-            res[tb] = (has_res && r < left) ? load_res4(e, mrow + t * kRowsPerPass, c_out)
+            res[tb] = (has_res && (kFull || r < left)) ? load_res4(e, mrow + t * kRowsPerPass, c_out)
                                             : make_float4(0.f, 0.f, 0.f, 0.f);
           } else if constexpr ((MD & 8) != 0) {
             const uint16_t* rp = static_cast<const uint16_t*>(e.res) + c_out;
@@ -691,7 +799,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         for (int tb = 0; tb < kResBatch; ++tb) {
           const int t = t0 + tb;
           const int r = r0 + t * kRowsPerPass;
-          if (r < left) {
+          if (kFull || r < left) {
             const float sa = s_sa[wm * kWT + j * 32 + r];
             const float4 v = *reinterpret_cast<const float4*>(tile + r * kPitch + pc);
             const float va[4] = {v.x, v.y, v.z, v.w};
@@ -735,6 +843,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
           }
         }
         }
+      };
+      if (col_ok) {
+        if (left >= 32) emit(std::true_type{});
+        else emit(std::false_type{});
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
@@ -1262,13 +1374,8 @@ __global__ __launch_bounds__(256) void pack_skinny_kernel(const uint8_t* __restr
   *reinterpret_cast<v4i*>(out + c * 16) = v;
 }
 
-// Large-M configurations:
-//  * wide:   256 x 256 tiles, 8 waves, 128-byte K stages, 2-deep ring
-//            (128 KB LDS, one workgroup per CU) -- shapes with many tiles;
-//  * narrow: 256 x 128 tiles, 4 waves, 64-byte stages, 3-deep ring (74 KB LDS,
-//            two workgroups per CU) -- twice the tiles, so fewer K splits
-//            (less partial-sum traffic) when the output is small.
-// Both need K % 128 == 0.
+// Large-M configurations (all with 128-byte K stages, so K % 128 == 0): see
+// pick_big below.
 constexpr int kBigKB = 128;
 
 // Every M past the skinny range (M > 64) with K % 128 == 0 takes gemm_big; its
@@ -1278,7 +1385,10 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 
 // Large-M configuration for a shape:
 //  * kWide / kWide192: 256 tokens x 256 (or 192) weight rows per workgroup, one
-//    workgroup per CU. 192-row tiles are taken (non-GLU only) when they need
+//    workgroup per CU. 256 x 256 tiles run the 4-wave register-pipelined form
+//    (C5 up 8192x14336x3072 GELU 341 -> 317 us, C5 qkv 247 -> 224 us, C3 gate|up
+//    73 -> 69 us against 8 waves of 128 x 64), or 8 waves when an operand
+//    spans 4 GiB or more (32-bit DMA offsets); 256 x 192 tiles use 8 waves. 192-row tiles are taken (non-GLU only) when they need
 //    fewer tile rounds on the 256 CUs, weighted by tile height and efficiency:
 //    e.g. an 8192 x 3072 output is 384 tiles of 256 rows (a half-empty second
 //    round) but 512 tiles of 192 rows (two full rounds): 329 -> 302 us for
@@ -1315,6 +1425,14 @@ inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
   return BigCfg::kWide;
 }
 
+// The 4-wave kernel forms DMA addresses as a 32-bit byte offset (row * ld, a
+// 24-bit multiply) from a wave-uniform base: both operands must span < 4 GiB
+// with rows and row strides below 2^24.
+inline bool dma32_ok(int64_t M, int64_t N, int64_t lda, int64_t ldw) {
+  constexpr int64_t k24 = int64_t(1) << 24, k32 = int64_t(1) << 32;
+  return M < k24 && N < k24 && lda < k24 && ldw < k24 && M * lda < k32 && N * ldw < k32;
+}
+
 template <bool GLU>
 int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K, const Epi& e, void* ws,
                  size_t ws_bytes, hipStream_t st) {
@@ -1323,6 +1441,8 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
       if constexpr (!GLU) return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       [[fallthrough]];
     case BigCfg::kWide:
+      if (dma32_ok(e.M, e.N, lda, ldw))
+        return launch_big<256, 256, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     case BigCfg::kSmall:
       return launch_big<64, 128, 128, 2, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);

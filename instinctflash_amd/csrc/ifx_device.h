@@ -147,6 +147,11 @@ __device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
 }
 
+// dma16 with the address split into a wave-uniform base (SGPR pair) and a
+// per-lane 32-bit byte offset: one VGPR per source instead of two.
+__device__ __forceinline__ void dma16s(const uint8_t* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base) : "memory", "m0");
+}
 
 // s_waitcnt vmcnt(N) for a compile-time N (0..63).
 template <int N>

@@ -151,6 +151,23 @@ def test_large_m_epilogue_combinations(gpu, oracle_mod, act, res, gate):
     _check(gpu, oracle_mod, qa, sa, w, f"{act} res={res} gate={gate}", ref_w=fw, act=act, residual=r, gate=gt)
 
 
+@pytest.mark.parametrize("M,N,K,act", [(4112, 12304, 128, None), (4112, 12304, 256, "gelu_tanh"),
+                                       (4112, 12304, 384, None), (3000, 16416, 640, "geglu"),
+                                       (2100, 24608, 128, "swiglu"), (8192, 6144, 1024, "gelu_tanh")])
+def test_wide_tile_k_loop_edges(gpu, oracle_mod, M, N, K, act):
+    # >= 192 tiles of 256 x 256: the 4-wave register-pipelined kernel, whose K
+    # loop has a prologue of two stages, a main part that issues the stage two
+    # ahead and a tail of up to two stages without DMA; K of 1..5 stages and
+    # 8 stages exercises every split of the three, ragged M and N clamp the
+    # DMA rows of the last tiles, GLU weights included
+    from instinctflash_amd.kernels import pack_glu
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
+    glu = act in ("geglu", "swiglu")
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    _check(gpu, oracle_mod, qa, sa, pack_glu(fw) if glu else fw, f"wide {M}x{N}x{K}", ref_w=fw, act=act,
+           residual=res)
+
+
 @pytest.mark.parametrize("K", [1024, 8192])
 @pytest.mark.parametrize("act,resgate", [("gelu_tanh", False), (None, True), ("swiglu", False)])
 def test_ragged_small_grid_configs(gpu, oracle_mod, K, act, resgate):
