@@ -491,7 +491,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int wn = wave / kWM;  // weight-row half
   const int wm = wave % kWM;  // token slice of kWT tokens
 
@@ -573,45 +573,51 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     //   is in LDS and slot kt is free);
     //   half 1: MFMAs on (kt, 1), reads of (kt+1, 0), and the DMA of stage
     //   kt+2 into slot kt, one instruction after each MFMA.
-    static_assert(KB == 128 && STAGES == 2 && kFN == 4 && kFM == 4 && kLoads == 16, "4-wave 128 x 128 layout");
-    // this wave's DMA sources: one operand (wave-uniform base) and a 32-bit byte
-    // offset per lane, formed per instruction (row clamp + multiply-add) so that
-    // no address registers stay live; the launch guarantees both operands span
-    // < 4 GiB and rows * ld < 2^24 * 2^24. DMA i of a stage covers tile rows
-    // 8*(wave*16 + i) + lrow; its chunk swizzle depends only on i's parity.
+    static_assert(KB == 128 && STAGES == 2 && kFM == 4 && (kFN == 3 || kFN == 4), "4-wave layout");
+    constexpr int kMF = kFN * kFM;        // MFMAs per half
+    constexpr int kRd = 2 * (kFN + kFM);  // 16-byte LDS reads per half
+    static_assert(kLoads <= kRd && kLoads % 2 == 0, "one DMA per LDS read");
+    // DMA sources: a wave-uniform choice of operand and a 32-bit byte offset
+    // per lane, formed per instruction (row clamp + 24-bit multiply-add) so no
+    // address registers stay live; the launch guarantees both operands span
+    // < 4 GiB with rows and row strides below 2^24. DMA i of a stage covers
+    // tile rows 8 * (wave * kLoads + i) + lrow (weight rows first).
     static_assert(kRowsPerDma == 8, "128-byte rows");
-    const bool dw = wave * kLoads * kRowsPerDma < BN;
-    const uintptr_t dsel = reinterpret_cast<uintptr_t>(dw ? W : A);
-    const uint8_t* dbase = reinterpret_cast<const uint8_t*>(
-        static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(dsel)))) |
-        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(dsel >> 32))))
-         << 32));
-    const int drow0 = (dw ? static_cast<int>(n0) + wave * kLoads * 8 : static_cast<int>(m0) + wave * kLoads * 8 - BN) + lrow;
-    const int dlast = static_cast<int>(dw ? n_last : m_last);
-    const uint32_t dld = static_cast<uint32_t>(dw ? ldw : lda);
-    const uint32_t dkc0 = static_cast<uint32_t>(kt0) * KB + ((lpos ^ lrow) << 4);        // even i
-    const uint32_t dkc1 = static_cast<uint32_t>(kt0) * KB + ((lpos ^ lrow ^ 1) << 4);    // odd i
+    const int iw = BN / 8 - wave * kLoads;  // DMAs i < iw of this wave load weight rows
+    uint32_t doff[kLoads];                  // per-lane byte offset of DMA i, stage kt0
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int blk = wave * kLoads + i;
+      const int r = blk * 8 + lrow;
+      const bool isw = i < iw;
+      const uint32_t row = static_cast<uint32_t>(isw ? min(n0 + r, n_last) : min(m0 + (r - BN), m_last));
+      doff[i] = __umul24(row, static_cast<uint32_t>(isw ? ldw : lda)) +
+                static_cast<uint32_t>(((lpos ^ lrow ^ (blk & 1)) << 4) + kt0 * KB);
+    }
+    const uint64_t wbase = reinterpret_cast<uintptr_t>(W), abase = reinterpret_cast<uintptr_t>(A);
     auto dma_one = [&](int kl, int i) {
-      const uint32_t row = static_cast<uint32_t>(min(drow0 + 8 * i, dlast));
-      const uint32_t off = __umul24(row, dld) + ((i & 1) ? dkc1 : dkc0) + static_cast<uint32_t>(kl) * KB;
-      dma16s(dbase, off, lds_base + (kl % STAGES) * kStage + i * 1024);
+      // branch-free wave-uniform choice of the operand base
+      const uint64_t sel = static_cast<uint64_t>(-static_cast<int64_t>(i < iw));
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(abase ^ ((wbase ^ abase) & sel));
+      dma16s(base, doff[i] + static_cast<uint32_t>(kl) * KB, lds_base + (kl % STAGES) * kStage + i * 1024);
     };
-    // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (8+2j, 9+2j)
-    v4i fr[2][16];
+    // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (2kFN+2j, 2kFN+2j+1)
+    v4i fr[2][kRd];
     auto read_one = [&](const uint8_t* base, v4i* f, int h, int r) {
       const int row = r < 2 * kFN ? wn * (32 * kFN) + (r >> 1) * 32 + frow : BN + wm * kWT + ((r - 2 * kFN) >> 1) * 32 + frow;
       f[r] = ld16(base + S::off(row, 4 * h + 2 * fhalf + (r & 1)));
     };
     auto mfma_one = [&](const v4i* f, int m) {
       const int i = m / kFM, j = m % kFM;
-      acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[8 + 2 * j], f[9 + 2 * j]), acc[i][j]);
+      acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[2 * kFN + 2 * j], f[2 * kFN + 2 * j + 1]), acc[i][j]);
     };
     auto interleave = [] {  // keep the MFMA / LDS-read alternation
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
+      for (int m = 0; m < kMF; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
+      if constexpr (kRd > kMF) __builtin_amdgcn_sched_group_barrier(0x100, kRd - kMF, 0);
     };
     auto wait_lgkm0 = [] { __builtin_amdgcn_s_waitcnt(0xC07F); };  // lgkmcnt(0), visible to the compiler
     auto sync = [&] {
@@ -631,15 +637,15 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
     sync();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) read_one(smem, fr[0], 0, r);
+    for (int r = 0; r < kRd; ++r) read_one(smem, fr[0], 0, r);
     auto stage = [&](int kt, auto dma_tag) {
       constexpr bool kDma = decltype(dma_tag)::value;  // stage kt + 2 exists
       const uint8_t* cur = smem + (kt % STAGES) * kStage;
       const uint8_t* nxt = smem + ((kt + 1) % STAGES) * kStage;  // after the last stage: a settled slot, unused
       wait_lgkm0();
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        mfma_one(fr[0], m);
+      for (int m = 0; m < kRd; ++m) {
+        if (m < kMF) mfma_one(fr[0], m);
         read_one(cur, fr[1], 1, m);
       }
       interleave();
@@ -647,10 +653,12 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       if (kDma || kt + 1 < nk) wait_vmcnt<0>();
       sync();
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        mfma_one(fr[1], m);
+      for (int m = 0; m < kRd; ++m) {
+        if (m < kMF) mfma_one(fr[1], m);
         read_one(nxt, fr[0], 0, m);
-        if constexpr (kDma) dma_one(kt + 2, m);
+        if constexpr (kDma) {
+          if (m < kLoads) dma_one(kt + 2, m);
+        }
       }
       interleave();
     };
@@ -1438,7 +1446,11 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
                  size_t ws_bytes, hipStream_t st) {
   switch (pick_big(e.M, e.N, K, GLU)) {
     case BigCfg::kWide192:
-      if constexpr (!GLU) return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      if constexpr (!GLU) {
+        if (dma32_ok(e.M, e.N, lda, ldw))
+          return launch_big<256, 192, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+        return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      }
       [[fallthrough]];
     case BigCfg::kWide:
       if (dma32_ok(e.M, e.N, lda, ldw))
