@@ -48,7 +48,12 @@ def device_arch(device=None, torch_mod=None) -> str | None:
     t = _torch(torch_mod)
     if not t.cuda.is_available():
         return None
-    idx = 0 if device is None else (getattr(device, "index", None) or 0)
+    if isinstance(device, int):
+        idx = device
+    elif isinstance(device, str):
+        idx = int(device.split(":")[1]) if ":" in device else 0
+    else:
+        idx = 0 if device is None else (getattr(device, "index", None) or 0)
     props = t.cuda.get_device_properties(idx)
     return getattr(props, "gcnArchName", None)
 
