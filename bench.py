@@ -235,6 +235,38 @@ def measure_engine(dev, reps=5):
             "ms_per_chunk": round(ms, 4), "kernels_per_chunk": launches}
 
 
+def measure_prefix(dev, layers=4, reps=5):
+    """The prefix stacks that define C3 (pi05 PaliGemma, 816 rows) and C4 (VLA4
+    Qwen2.5, 1024 rows) end to end on these kernels (instinctflash_amd/
+    prefix.py; reference engines/pi05/engine.py:192-216, engines/vla4/
+    engine.py:114-139): `layers` decoder layers of random weights captured in
+    one graph; µs per layer and the layer's FP8 GEMM TFLOP/s."""
+    import torch
+    from instinctflash_amd.prefix import PI05_PREFIX, VLA4_PREFIX, PrefixStack, random_prefix_weights
+    out = {}
+    for cfg, M in ((PI05_PREFIX, 816), (VLA4_PREFIX, 1024)):
+        st = PrefixStack(cfg, random_prefix_weights(cfg, layers, dev, seed=0), dev, smax=M)
+        st.set_prefix(M)
+        x = torch.randn(M, cfg.D, generator=torch.Generator().manual_seed(1)).to(dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            st.forward(x, M)
+        torch.cuda.current_stream().wait_stream(side)
+        g = capture(lambda i: st.forward(x, M), 1, side)
+        time_graph(g)
+        ms = sorted(time_graph(g)[0] for _ in range(reps))[reps // 2]
+        flops = 2 * M * cfg.D * (cfg.qkv_n + cfg.HQ * cfg.HD + 3 * cfg.FF)  # qkv, o, gate|up, down
+        us = ms * 1e3 / layers
+        out[cfg.name] = {"rows": M, "layers": layers, "us_per_layer": round(us, 2),
+                         "gemm_tflops": round(flops / us / 1e6, 1),
+                         "kernels_per_layer": 9}
+        _log(f"[bench] {cfg.name}: {us:.1f} us per layer ({flops / us / 1e6:.0f} TFLOP/s of FP8 GEMM)")
+        del st, g
+        torch.cuda.empty_cache()
+    return out
+
+
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -455,6 +487,7 @@ def main():
     if not args.no_others:
         out["producers"] = measure_producers(dev)
         out["engine"] = measure_engine(dev)
+        out["prefix"] = measure_prefix(dev)
     if not args.no_cpu:
         for key in order:
             _log(f"[bench] CPU baseline {key} (reference CPU FP8 path)")
