@@ -728,7 +728,9 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   // its MFMAs and publishes the token scales.
   constexpr int kCols = GLU ? 16 * kFN : 32 * kFN;  // output columns of a wave tile
   constexpr int kLanesPerRow = kCols / 4;
-  constexpr int kRowsPerPass = 64 / kLanesPerRow;
+  // whole rows per 64-lane pass, a power of two (12 lanes per row for 192-row
+  // GLU tiles: 4 rows, 16 lanes idle)
+  constexpr int kRowsPerPass = 64 / kLanesPerRow >= 8 ? 8 : 64 / kLanesPerRow >= 4 ? 4 : 64 / kLanesPerRow >= 2 ? 2 : 1;
   constexpr int kRowIters = 32 / kRowsPerPass;
   static_assert(32 % kRowsPerPass == 0, "epilogue row passes");
   const int64_t nw = n0 + wn * (32 * kFN);                // first (packed) weight row of the wave tile
@@ -1396,11 +1398,11 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 //    workgroup per CU. 256 x 256 tiles run the 4-wave register-pipelined form
 //    (C5 up 8192x14336x3072 GELU 341 -> 317 us, C5 qkv 247 -> 224 us, C3 gate|up
 //    73 -> 69 us against 8 waves of 128 x 64), or 8 waves when an operand
-//    spans 4 GiB or more (32-bit DMA offsets); 256 x 192 tiles use 8 waves. 192-row tiles are taken (non-GLU only) when they need
+//    spans 4 GiB or more (32-bit DMA offsets); 256 x 192 tiles likewise. 192-row tiles are taken when they need
 //    fewer tile rounds on the 256 CUs, weighted by tile height and efficiency:
 //    e.g. an 8192 x 3072 output is 384 tiles of 256 rows (a half-empty second
 //    round) but 512 tiles of 192 rows (two full rounds): 329 -> 302 us for
-//    K = 14336.
+//    K = 14336; a GLU output of 1024 x 22016 is 344 tiles of 256 but 460 of 192.
 //  * kSmall: fewer than 192 tiles of 256 x 256 and K <= 4096 -- 64 tokens x
 //    128 weight rows, 128-byte stages, 4 waves of 64 x 32 (short MFMA chains
 //    per wave: the loop is latency-bound at these sizes), two workgroups per
@@ -1424,7 +1426,8 @@ inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
     if (K > 4096) return BigCfg::kNarrow;
     return ((M + 63) / 64) * ((N + 127) / 128) < 256 ? BigCfg::kSmall32 : BigCfg::kSmall;
   }
-  if (!glu) {
+  (void)glu;  // GLU tiles take the same shapes (16-row gate|up blocks divide 192)
+  {
     const int64_t t192 = tm * ((N + 191) / 192);
     // a 192-row tile does ~15% less work per unit time than a 256-row one
     // (measured: 8192x9216x3072, 6 full rounds of 192 vs 4.5 of 256, is 2.5% slower)
@@ -1446,12 +1449,10 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
                  size_t ws_bytes, hipStream_t st) {
   switch (pick_big(e.M, e.N, K, GLU)) {
     case BigCfg::kWide192:
-      if constexpr (!GLU) {
-        if (dma32_ok(e.M, e.N, lda, ldw))
-          return launch_big<256, 192, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
-        return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
-      }
-      [[fallthrough]];
+      if (dma32_ok(e.M, e.N, lda, ldw))
+        return launch_big<256, 192, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      if constexpr (!GLU) return launch_big<256, 192, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      [[fallthrough]];  // operands past 4 GiB with GLU: 8 waves of 256 x 256 (no split at this size)
     case BigCfg::kWide:
       if (dma32_ok(e.M, e.N, lda, ldw))
         return launch_big<256, 256, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
