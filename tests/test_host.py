@@ -173,3 +173,17 @@ def test_permute_rope_rows_on_cpu_tensors():
     assert p.rope == (hq, hkv, hd)
     with pytest.raises(ValueError):
         permute_rope_rows(Fp8Weight(w, scale), hq, hkv + 1, hd)
+
+
+def test_wan_rope_tables_sections_and_ladders():
+    # 3-D rotary of the Wan blocks (reference engines/wan_va/weights.py:76-84):
+    # 128-dim heads split their 64 channel pairs 22 / 21 / 21 over frame, height
+    # and width; each section's ladder starts at 1 and falls by theta^(-2/d)
+    from instinctflash_amd.wan_block import wan_rope_tables
+    inv, sec = wan_rope_tables(128, 10000.0)
+    assert inv.dtype == torch.float32 and sec.dtype == torch.int32 and inv.numel() == sec.numel() == 64
+    assert [int((sec == s).sum()) for s in range(3)] == [22, 21, 21]
+    for s, d in ((0, 44), (1, 42), (2, 42)):
+        f = inv[sec == s].double()
+        assert f[0] == 1.0
+        assert torch.allclose(f[1:] / f[:-1], torch.full_like(f[1:], 10000.0 ** (-2.0 / d)), rtol=1e-6)
