@@ -168,10 +168,11 @@ int ifx_moe_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const 
                       float* scale, void* stream);
 
 /*
- * y[m,d] = x[m,d] * row[m] * col[d] + bias[d], x bf16, y bf16 or f32 (y_dtype).
- * Replaces: instinctflash/kernels/norm.py:178-185 `dequant_rows`.
+ * y[m,d] = x[m,d] * row[m] * col[d] + bias[d] in float32 (one rounding per
+ * operation, in that order); x and y each bf16, f16 or f32 (x_dtype, y_dtype).
+ * Replaces: instinctflash/kernels/norm.py:178-185 `dequant_rows` (any float dtypes).
  */
-int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const float* row,
+int ifx_dequant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t D, const float* row,
                      const float* col, const float* bias, void* y, int y_dtype, int64_t ldy,
                      void* stream);
 

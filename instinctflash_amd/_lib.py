@@ -69,7 +69,7 @@ SIGNATURES = {
     "ifx_pack_tensor_bf16": (_INT, [_P, _I64, _P, _P, _P]),
     "ifx_row_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _I64, _P, _P]),
     "ifx_gated_act_quant": (_INT, [_P, _I64, _I64, _I64, _P, _P, _INT, _P, _I64, _P, _P]),
-    "ifx_dequant_rows": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P]),
+    "ifx_dequant_rows": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _I64, _P]),
     "ifx_fp8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "ifx_quant_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT, _INT]),
     "ifx_fp8_skinny_tiled_bytes": (_SZ, [_I64, _I64]),

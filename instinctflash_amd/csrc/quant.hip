@@ -474,19 +474,27 @@ __global__ __launch_bounds__(kBlock) void tensor_pack_vec(const uint16_t* x, int
 
 // ---- dequant_rows / GLU weight repack --------------------------------------
 
-__global__ __launch_bounds__(kBlock) void dequant_rows_kernel(const uint16_t* x, int64_t ldx,
+__device__ __forceinline__ float load_any(const void* base, int dtype, int64_t i) {
+  if (dtype == IFX_DTYPE_F32) return static_cast<const float*>(base)[i];
+  if (dtype == IFX_DTYPE_F16) return static_cast<float>(static_cast<const _Float16*>(base)[i]);
+  return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
+}
+
+__global__ __launch_bounds__(kBlock) void dequant_rows_kernel(const void* x, int x_dtype, int64_t ldx,
                                                              int64_t M, int64_t D, const float* row,
                                                              const float* col, const float* bias,
-                                                             void* y, int y_f32, int64_t ldy) {
+                                                             void* y, int y_dtype, int64_t ldy) {
   const int64_t m = blockIdx.y;
   const int64_t d = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   if (d >= D) return;
-  float v = bf16_bits_to_f32(x[m * ldx + d]);
+  float v = load_any(x, x_dtype, m * ldx + d);
   if (row) v = v * row[m];
   if (col) v = v * col[d];
   if (bias) v = v + bias[d];
-  if (y_f32) static_cast<float*>(y)[m * ldy + d] = v;
-  else static_cast<uint16_t*>(y)[m * ldy + d] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  const int64_t o = m * ldy + d;
+  if (y_dtype == IFX_DTYPE_F32) static_cast<float*>(y)[o] = v;
+  else if (y_dtype == IFX_DTYPE_F16) static_cast<_Float16*>(y)[o] = static_cast<_Float16>(v);
+  else static_cast<uint16_t*>(y)[o] = static_cast<uint16_t>(f32_to_bf16_bits(v));
 }
 
 // One block per packed row p: source row = gate or up row per the 16-row interleave.
@@ -673,17 +681,17 @@ int ifx_moe_act_quant(const void* gu, int64_t ldgu, int64_t M, int64_t F, const 
                        F, static_cast<uint8_t*>(q), ldq, scale, st);
 }
 
-int ifx_dequant_rows(const void* x, int64_t ldx, int64_t M, int64_t D, const float* row,
+int ifx_dequant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t D, const float* row,
                      const float* col, const float* bias, void* y, int y_dtype, int64_t ldy,
                      void* stream) {
   if (M < 0 || D < 0 || ldx < D || ldy < D || M > 65535) return IFX_ERR_INVALID;
-  if (y_dtype != IFX_DTYPE_BF16 && y_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
+  for (int dt : {x_dtype, y_dtype})
+    if (dt != IFX_DTYPE_BF16 && dt != IFX_DTYPE_F32 && dt != IFX_DTYPE_F16) return IFX_ERR_INVALID;
   if (M == 0 || D == 0) return IFX_OK;
   if (!x || !y) return IFX_ERR_INVALID;
   const dim3 grid(static_cast<unsigned>((D + kBlock - 1) / kBlock), static_cast<unsigned>(M));
-  hipLaunchKernelGGL(dequant_rows_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), ldx, M, D, row, col, bias, y,
-                     y_dtype == IFX_DTYPE_F32 ? 1 : 0, ldy);
+  hipLaunchKernelGGL(dequant_rows_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), x, x_dtype, ldx,
+                     M, D, row, col, bias, y, y_dtype, ldy);
   return launch_status();
 }
 

@@ -34,20 +34,24 @@ def row_quant(x, q, q_scale, *, row=None, col=None, bias=None, gelu=False, num_w
                                          _stream(x.device)), "ifx_row_quant")
 
 
+_FLOAT_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
 def dequant_rows(x, y, *, row=None, col=None, bias=None, block=None, num_warps=4):
-    """y[m] = x[m] * row[m] * col + bias; x bf16, y bf16 or fp32.
+    """y[m] = x[m] * row[m] * col + bias in float32; x and y bf16, fp16 or fp32
+    (any combination).
 
     Reference: instinctflash/kernels/norm.py:178-185."""
-    M, D, ldx = _rows("x", x, torch.bfloat16)
-    if y.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("y must be bf16 or fp32")
+    if x.dtype not in _FLOAT_DTYPES or y.dtype not in _FLOAT_DTYPES:
+        raise ValueError("dequant_rows takes bf16, fp16 or fp32 x and y")
+    M, D, ldx = _rows("x", x, x.dtype)
     _, _, ldy = _rows("y", y, y.dtype, x.device, cols=D)
     _vec("row", row, M, device=x.device)
     _vec("col", col, D, device=x.device)
     _vec("bias", bias, D, device=x.device)
-    dt = _lib.DTYPE_F32 if y.dtype == torch.float32 else _lib.DTYPE_BF16
-    _lib.check(_lib.load().ifx_dequant_rows(_ptr(x), ldx, M, D, _ptr(row), _ptr(col), _ptr(bias), _ptr(y),
-                                            dt, ldy, _stream(x.device)), "ifx_dequant_rows")
+    _lib.check(_lib.load().ifx_dequant_rows(_ptr(x), _FLOAT_DTYPES[x.dtype], ldx, M, D, _ptr(row), _ptr(col),
+                                            _ptr(bias), _ptr(y), _FLOAT_DTYPES[y.dtype], ldy, _stream(x.device)),
+               "ifx_dequant_rows")
 
 
 def _table(name, t, D, rows_from_index, device):

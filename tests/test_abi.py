@@ -114,7 +114,8 @@ def test_contract_violations_rejected_before_launch(lib):
     assert ql(64, _lib.SCALE_ROW, 0, 100, 64) == _lib.ERR_WORKSPACE
     assert ql(64, _lib.SCALE_ROW, 0, 16, 64) == _lib.ERR_WORKSPACE
     assert ql(64, _lib.SCALE_ROW, 0, 0, 64) == _lib.OK
-    assert lib.ifx_dequant_rows(fake, 64, 1, 64, None, None, None, fake, 9, 64, None) == _lib.ERR_INVALID
+    assert lib.ifx_dequant_rows(fake, 0, 64, 1, 64, None, None, None, fake, 9, 64, None) == _lib.ERR_INVALID
+    assert lib.ifx_dequant_rows(fake, 7, 64, 1, 64, None, None, None, fake, 0, 64, None) == _lib.ERR_INVALID
 
 
 def test_loader_rejects_missing_library(tmp_path):

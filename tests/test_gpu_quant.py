@@ -273,6 +273,20 @@ def test_dequant_rows(gpu):
     yb = torch.empty((M, D), dtype=torch.bfloat16, device=gpu)
     dequant_rows(x.to(gpu), yb, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
     assert torch.equal(yb.cpu(), exp.to(torch.bfloat16))
+    # any float dtypes in and out (the reference's GR00T engine writes fp16 q|k|v
+    # and cross K/V): float32 arithmetic in the same order, one rounding at the store
+    for xd in (torch.float16, torch.float32):
+        for yd in (torch.float16, torch.bfloat16, torch.float32):
+            xs = x.to(xd)
+            yo = torch.empty((M, D), dtype=yd, device=gpu)
+            dequant_rows(xs.to(gpu), yo, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
+            ex = ((xs.float() * row[:, None]) * col + bias).to(yd)
+            assert torch.equal(yo.cpu(), ex), (xd, yd)
+    # strided rows (a column slice of a wider accumulator)
+    wide = torch.randn((M, 3 * D // 2), generator=g).to(torch.bfloat16)
+    ys = torch.empty((M, D // 2), dtype=torch.float16, device=gpu)
+    dequant_rows(wide.to(gpu)[:, D:], ys, col=col[: D // 2].to(gpu))
+    assert torch.equal(ys.cpu(), (wide[:, D:].float() * col[: D // 2]).to(torch.float16))
 
 
 def test_graph_replay_matches_eager(gpu, oracle_mod):
