@@ -131,10 +131,11 @@ int ifx_pack_tensor_bf16(const void* x, int64_t count, const float* scale, void*
 /* Flags of ifx_row_quant. */
 #define IFX_RQ_GELU 1 /* gelu_tanh after the affine terms */
 #define IFX_RQ_F16 2  /* x holds fp16 (default bf16) */
+#define IFX_RQ_F32 4  /* x holds float32 (the GR00T engine's encoder rows, engines/groot_n17/engine.py:144) */
 
 /*
- * Consumer-side producer of the next FP8 operand from a raw bf16 (or fp16)
- * accumulator:
+ * Consumer-side producer of the next FP8 operand from a raw bf16 (or fp16,
+ * float32) accumulator:
  *   v = x[m,k] * row[m] * col[k] + bias[k]   (NULL factors are skipped)
  *   v = gelu_tanh(v) with IFX_RQ_GELU
  *   (q[m,:], scale[m]) = quantize(v) with the recipe above (FP32 v, no bf16 rounding).

@@ -32,6 +32,7 @@ LD_TILED = 0  # row stride selecting the skinny tile layout of an e4m3 output
 
 RQ_GELU = 1
 RQ_F16 = 2
+RQ_F32 = 4
 
 ACT_GELU_TANH = 0
 ACT_SILU = 1

@@ -100,6 +100,7 @@ struct SrcAffine {
   const float* bias;
   int gelu;
   int f16;  // x holds fp16 (else bf16)
+  int f32;  // x holds float32 (element path only)
   struct Raw { uint4 a; Vec8 c, b; };
   __device__ __forceinline__ void unpack(const uint4& r, float* v) const {
     if (!f16) {
@@ -114,6 +115,7 @@ struct SrcAffine {
     }
   }
   __device__ __forceinline__ float elem(int64_t m, int64_t k) const {
+    if (f32) return reinterpret_cast<const float*>(x)[m * ldx + k];
     const uint16_t h = x[m * ldx + k];
     return f16 ? static_cast<float>(__builtin_bit_cast(_Float16, h)) : bf16_bits_to_f32(h);
   }
@@ -628,10 +630,12 @@ int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float*
                   const float* col, const float* bias, int flags, void* q, int64_t ldq,
                   float* scale, void* stream) {
   if (M < 0 || K < 0 || ldx < K || (ldq != IFX_LD_TILED && ldq < K)) return IFX_ERR_INVALID;
-  if (flags & ~(IFX_RQ_GELU | IFX_RQ_F16)) return IFX_ERR_INVALID;
+  if (flags & ~(IFX_RQ_GELU | IFX_RQ_F16 | IFX_RQ_F32) || (flags & IFX_RQ_F16 && flags & IFX_RQ_F32))
+    return IFX_ERR_INVALID;
   if (M > 0 && (!x || !q || !scale)) return IFX_ERR_INVALID;
-  const bool vec_ok = aligned16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 && ldq % 8 == 0 &&
-                      aligned16(col) && aligned16(bias);
+  const bool f32 = (flags & IFX_RQ_F32) != 0;
+  const bool vec_ok = !f32 && aligned16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0 &&
+                      ldq % 8 == 0 && aligned16(col) && aligned16(bias);
   auto go = [&](auto s) {
     s.x = static_cast<const uint16_t*>(x);
     s.ldx = ldx;
@@ -640,6 +644,7 @@ int ifx_row_quant(const void* x, int64_t ldx, int64_t M, int64_t K, const float*
     s.bias = bias;
     s.gelu = (flags & IFX_RQ_GELU) ? 1 : 0;
     s.f16 = (flags & IFX_RQ_F16) ? 1 : 0;
+    s.f32 = f32 ? 1 : 0;
     return dispatch_rows(s, vec_ok, M, K, static_cast<uint8_t*>(q), ldq, scale, static_cast<hipStream_t>(stream));
   };
   if (col) return bias ? go(SrcAffine<true, true>{}) : go(SrcAffine<true, false>{});

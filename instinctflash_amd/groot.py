@@ -277,7 +277,7 @@ class GrootHead:
             count.copy_(sel.sum().to(torch.int32).view(1))
         for key in ("text", "image"):
             src = self.enc[key][:M]
-            quant_rows(src, q8(M, VL_D), s0)
+            row_quant(src, q8(M, VL_D), s0)
             note("enc_quant", x=src, q=q8(M, VL_D), s=s0)
             for i, blk in enumerate(self.w.dit):
                 if not blk.cross or blk.text != (key == "text"):

@@ -18,17 +18,19 @@ from .fp8 import E4M3, _ptr, _qout, _rows, _stream, _vec
 def row_quant(x, q, q_scale, *, row=None, col=None, bias=None, gelu=False, num_warps=None):
     """q[m] = fp8((x[m] * row[m] * col + bias) [-> gelu_tanh] / s[m]) with per-row s.
 
-    Reference: instinctflash/kernels/norm.py:150-158. ``x`` is bf16, or fp16
-    (the pi05 engine's attention output, engines/pi05/engine.py:205)."""
-    if x.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError("row_quant expects bf16 or fp16 input")
+    Reference: instinctflash/kernels/norm.py:150-158. ``x`` is bf16, fp16
+    (the pi05 engine's attention output, engines/pi05/engine.py:205) or
+    float32 (the GR00T engine's encoder rows, engines/groot_n17/engine.py:144)."""
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError("row_quant expects bf16, fp16 or fp32 input")
     M, D, ldx = _rows("x", x, x.dtype)
     qp, ldq = _qout("q", q, M, D, x.device)
     _vec("q_scale", q_scale, M, device=x.device)
     _vec("row", row, M, device=x.device)
     _vec("col", col, D, device=x.device)
     _vec("bias", bias, D, device=x.device)
-    flags = (_lib.RQ_GELU if gelu else 0) | (_lib.RQ_F16 if x.dtype == torch.float16 else 0)
+    flags = (_lib.RQ_GELU if gelu else 0) | (_lib.RQ_F16 if x.dtype == torch.float16 else 0) | \
+        (_lib.RQ_F32 if x.dtype == torch.float32 else 0)
     _lib.check(_lib.load().ifx_row_quant(_ptr(x), ldx, M, D, _ptr(row), _ptr(col), _ptr(bias),
                                          flags, qp, ldq, _ptr(q_scale),
                                          _stream(x.device)), "ifx_row_quant")

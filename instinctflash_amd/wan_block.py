@@ -153,7 +153,7 @@ class WanStack:
         rows, D = B * self.TEXT, self.D
         th = text_h.reshape(rows, D).float().contiguous()
         s = self.scale[0][:rows]
-        quant_rows(th, self.q8v(rows, D), s)
+        row_quant(th, self.q8v(rows, D), s)
         note("text_quant", x=th, q=self.q8v(rows, D), s=s)
         for i, blk in enumerate(self.blocks):
             raw = self.rawv(rows, 2 * D)

@@ -240,6 +240,26 @@ def test_row_quant_fp16_input(gpu, oracle_mod, M, D):
     assert np.array_equal(_q(q), eq) and np.array_equal(_f(s), es)
 
 
+@pytest.mark.parametrize("M,D", [(96, 2048), (5, 1000)])
+def test_row_quant_fp32_input(gpu, oracle_mod, M, D):
+    # the GR00T engine quantizes its float32 encoder rows (engines/groot_n17/engine.py:144):
+    # bytes and scales bit-exact to the oracle recipe, also with the affine terms
+    from instinctflash_amd.kernels import row_quant
+    g = torch.Generator().manual_seed(M * D)
+    x = torch.randn((M, D), generator=g) * 3
+    x[1] = 0.0  # an all-zero row takes the scale floor
+    q = torch.empty((M, D), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    row_quant(x.to(gpu), q, s)
+    eq, es = oracle_mod.quant_rows(x.numpy())
+    assert np.array_equal(_q(q), eq) and np.array_equal(_f(s).view(np.uint32), es.view(np.uint32))
+    row, col, bias = torch.rand(M, generator=g) + 0.5, torch.rand(D, generator=g) + 0.5, torch.randn(D, generator=g)
+    row_quant(x.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu), bias=bias.to(gpu))
+    v = ((x.numpy() * row.numpy()[:, None]).astype(np.float32) * col.numpy()[None, :]).astype(np.float32)
+    eq, es = oracle_mod.quant_rows((v + bias.numpy()[None, :]).astype(np.float32))
+    assert np.array_equal(_q(q), eq) and np.array_equal(_f(s).view(np.uint32), es.view(np.uint32))
+
+
 @pytest.mark.parametrize("act", [0, 1])
 def test_gated_act_quant(gpu, oracle_mod, act):
     from instinctflash_amd.kernels import gated_act_quant
