@@ -150,11 +150,16 @@ class Pi05Expert:
         self.kv_len.fill_(n + self.chunk)
         torch.arange(n, n + self.chunk, out=self.pos_chunk[:, 0])
 
-    def forward(self, noise=None):
+    def forward(self, noise=None, on_call=None):
         """Reference engine.py:212-245 (`_expert`); call for call with
-        ``reference_calls``, else the tile-layout form of the same math."""
+        ``reference_calls``, else the tile-layout form of the same math.
+        ``on_call`` (reference calls only) is called after every kernel with its
+        name and the buffers it read and wrote, for per-call parity tests."""
         if not self.reference_calls:
+            if on_call is not None:
+                raise ValueError("on_call needs reference_calls=True")
             return self._forward_tiled(noise)
+        note = on_call or (lambda name, **t: None)
         w, A = self.w, self.chunk
         q8, raw, s = self.q8v, self.rawv, self.scale
         if noise is not None:
@@ -166,31 +171,49 @@ class Pi05Expert:
         for step in range(w.steps):
             torch.addmm(w.action_in_b, self.x_t, self.in_w_t, out=self.dx)
             ma, mf = w.mod_attn[step], w.mod_ffn[step]
+            note("pre_res", res=self.dx)
             residual_norm_quant(self.dx, mod_scale=ma[0, 0], mod_shift=ma[0, 1], q=q8(A, EX_D), q_scale=s[0])
+            note("norm", res=self.dx, mod=(ma[0, 0], ma[0, 1]), q=q8(A, EX_D), s=s[0])
             for i, L in enumerate(w.layers):
                 gemm(q8(A, EX_D), L.qkv, raw(A, QKV_N))
+                note("gemm", a=q8(A, EX_D), w=L.qkv, out=raw(A, QKV_N))
                 qkv_split(raw(A, QKV_N), self.q16[:A], self.kc[i], self.vc[i], heads_q=HEADS, heads_kv=1,
                           head_dim=HEAD_DIM, inv_freq=self.inv_freq, pos=self.pos_chunk, row=s[0],
                           col=L.qkv.scale, kv_base=self.prefix_len)
+                note("qkv_split", raw=raw(A, QKV_N), row=s[0], w=L.qkv, q=self.q16[:A], k=self.kc[i], v=self.vc[i])
                 attention(qv, self.kc[i][None], self.vc[i][None], out=ov, kv_len=self.kv_len,
                           scale=HEAD_DIM ** -0.5)
+                note("attention", q=qv, k=self.kc[i][None], v=self.vc[i][None], out=ov, kv_len=self.kv_len)
                 row_quant(self.o16[:A], q8(A, HEADS * HEAD_DIM), s[1])
+                note("row_quant", x=self.o16[:A], q=q8(A, HEADS * HEAD_DIM), s=s[1])
                 gemm(q8(A, HEADS * HEAD_DIM), L.o, raw(A, EX_D))
+                note("gemm", a=q8(A, HEADS * HEAD_DIM), w=L.o, out=raw(A, EX_D))
+                note("pre_res", res=self.dx)
                 residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.o.scale,
                                     gate=ma[i, 2], mod_scale=mf[i, 0], mod_shift=mf[i, 1],
                                     q=q8(A, EX_D), q_scale=s[0])
+                note("norm", res=self.dx, delta=raw(A, EX_D), delta_row=s[1], w=L.o, gate=ma[i, 2],
+                     mod=(mf[i, 0], mf[i, 1]), q=q8(A, EX_D), s=s[0])
                 gemm(q8(A, EX_D), L.gate_up, raw(A, 2 * EX_FF))
+                note("gemm", a=q8(A, EX_D), w=L.gate_up, out=raw(A, 2 * EX_FF))
                 gated_act_quant(raw(A, 2 * EX_FF), q8(A, EX_FF), s[1], row=s[0], col=L.gate_up.scale,
                                 act=GELU_TANH)
+                note("gated_act_quant", gu=raw(A, 2 * EX_FF), row=s[0], w=L.gate_up, q=q8(A, EX_FF), s=s[1])
                 gemm(q8(A, EX_FF), L.down, raw(A, EX_D))
+                note("gemm", a=q8(A, EX_FF), w=L.down, out=raw(A, EX_D))
+                note("pre_res", res=self.dx)
                 if i < last:
                     residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
                                         gate=mf[i, 2], mod_scale=ma[i + 1, 0], mod_shift=ma[i + 1, 1],
                                         q=q8(A, EX_D), q_scale=s[0])
+                    note("norm", res=self.dx, delta=raw(A, EX_D), delta_row=s[1], w=L.down, gate=mf[i, 2],
+                         mod=(ma[i + 1, 0], ma[i + 1, 1]), q=q8(A, EX_D), s=s[0])
                 else:
                     mfin = w.mod_final[step]
                     residual_norm_quant(self.dx, delta=raw(A, EX_D), delta_row=s[1], delta_col=L.down.scale,
                                         gate=mf[i, 2], mod_scale=mfin[0], mod_shift=mfin[1], y=self.dy)
+                    note("norm", res=self.dx, delta=raw(A, EX_D), delta_row=s[1], w=L.down, gate=mf[i, 2],
+                         mod=(mfin[0], mfin[1]), y=self.dy)
             self.x_t.addmm_(self.dy, self.out_w_dt).add_(self.out_b_dt)
         return self.x_t
 

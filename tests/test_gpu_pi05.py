@@ -1,7 +1,8 @@
 """The pi05 action expert loop (reference instinctflash/engines/pi05/engine.py:
 212-245) on the gfx950 kernels, end to end.
 
-Checks: (1) against a plain PyTorch fp32 restatement of the same layer math
+Checks: (0) every kernel call of the reference call sequence against the
+oracle on the inputs it received (``_Checker`` below); (1) against a plain PyTorch fp32 restatement of the same layer math
 (dequantized FP8 weights, unquantized activations, fp32 attention and RoPE) --
 the FP8 activation rounding of every projection input makes this a tolerance
 check: cosine >= 0.999 on the residual stream and the actions after 2 layers x
@@ -150,3 +151,91 @@ def test_real_shapes_under_graph(gpu):
     graph.replay()
     torch.cuda.synchronize()
     assert torch.isfinite(eng.x_t).all() and eng.x_t.abs().max() < 1e4
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _u8(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+class _Checker:
+    """Each kernel call of the reference-call form against the oracle on the
+    inputs it received: residual updates bit-exact (float32, reference order),
+    e4m3 rows within 7% of the row max of the oracle's float64 RMSNorm + AdaLN
+    (tests/test_gi_kernels.py:112), y within 1e-5; GEMMs max|d| <= 2e-2 rms +
+    one bf16 rounding, cosine >= 0.9999; qkv_split within 2^-10 relative (fp16)
+    at the cache rows after the prefix; attention within 2e-3; row_quant bytes
+    and scales bit-exact; gated_act_quant (hardware exp in GELU) scales within 8
+    ulp, >= 99.9% identical bytes, within 7% of the row max."""
+
+    def __init__(self, oracle, eng, prefix):
+        self.o, self.eng, self.prefix = oracle, eng, prefix
+        self.pre = None
+        self.seen = []
+
+    def __call__(self, name, **t):
+        import numpy as np
+        from instinctflash_amd.pi05 import HEAD_DIM, HEADS
+        torch.cuda.synchronize()
+        o, A, P = self.o, self.eng.chunk, self.prefix
+        self.seen.append(name)
+        if name == "pre_res":
+            self.pre = _np(t["res"])
+        elif name == "norm":
+            kw = dict(mod_scale=_np(t["mod"][0]), mod_shift=_np(t["mod"][1]))
+            if "delta" in t:
+                kw.update(delta=_np(t["delta"]), delta_row=_np(t["delta_row"]), delta_col=_np(t["w"].scale),
+                          gate=_np(t["gate"]))
+            x_ref, y_ref = o.residual_norm(self.pre, **kw)
+            assert np.array_equal(_np(t["res"]).view(np.uint32), x_ref.view(np.uint32)), "residual not bit-exact"
+            if "q" in t:
+                deq = o.e4m3_decode(_u8(t["q"])) * _np(t["s"])[:, None]
+                assert (np.abs(deq - y_ref).max(axis=1) / np.abs(y_ref).max(axis=1)).max() < 0.07
+            else:
+                err = (np.abs(_np(t["y"]) - y_ref).max(axis=1) / np.abs(y_ref).max(axis=1)).max()
+                assert err <= 1e-5, f"y rel err {err:.3e}"
+        elif name == "gemm":
+            ref = o.ref_linear(_u8(t["a"]), None, _u8(t["w"].w), None)
+            got = _np(t["out"])
+            _, cos = o.parity_stats(got, ref)
+            rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+            excess = np.abs(got - ref) - (2e-2 * rms + 2.0 ** -8 * np.abs(ref))
+            assert excess.max() <= 0 and cos >= 0.9999, f"gemm {t['w'].w.shape}: {excess.max():.3e} {cos:.7f}"
+        elif name == "qkv_split":
+            q, k, v = o.qkv_split(_np(t["raw"]), HEADS, 1, HEAD_DIM, row=_np(t["row"]), col=_np(t["w"].scale),
+                                  inv_freq=_np(self.eng.inv_freq), pos=_np(self.eng.pos_chunk))
+            for nm, got, ref in (("q", t["q"], q), ("k", t["k"][P:P + A], k), ("v", t["v"][P:P + A], v)):
+                err = np.abs(_np(got).astype(np.float64) - ref) - (2.0 ** -10 * np.abs(ref) + 2e-5)
+                assert err.max() <= 0, f"qkv_split {nm}: excess {err.max():.3e}"
+        elif name == "attention":
+            n = int(t["kv_len"].item())
+            ref = o.attention(_np(t["q"]), _np(t["k"][:, :n]), _np(t["v"][:, :n]), np.full(A, n), HEAD_DIM ** -0.5)
+            err = np.abs(_np(t["out"]) - ref).max()
+            assert err < 2e-3, f"attention: max |d| {err:.3e}"
+        elif name == "row_quant":
+            eq, es = o.quant_rows(_np(t["x"]))
+            assert np.array_equal(_u8(t["q"]), eq) and np.array_equal(_np(t["s"]).view(np.uint32), es.view(np.uint32))
+        elif name == "gated_act_quant":
+            F = t["gu"].shape[1] // 2
+            x = _np(t["gu"]) * _np(t["row"])[:, None] * _np(t["w"].scale)[None, :]
+            h = o.gelu_tanh(x[:, :F].astype(np.float32)) * x[:, F:].astype(np.float32)
+            eq, es = o.quant_rows(h.astype(np.float32))
+            s = _np(t["s"])
+            assert np.all(np.abs(s.view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
+            assert (_u8(t["q"]) == eq).mean() > 0.999
+            deq = o.e4m3_decode(_u8(t["q"])) * s[:, None]
+            assert (np.abs(deq - h) / np.abs(h).max(axis=1, keepdims=True)).max() < 0.07
+        else:
+            raise AssertionError(f"unchecked call {name}")
+
+
+def test_expert_calls_against_oracle(gpu, oracle_mod):
+    # every kernel call of 2 layers x 2 steps, reference call sequence
+    eng, noise = _engine(gpu, layers=2, steps=2, prefix=300, smax=512, seed=11, reference_calls=True)
+    chk = _Checker(oracle_mod, eng, 300)
+    x = eng.forward(noise, on_call=chk)
+    assert chk.seen.count("gated_act_quant") == 4 and chk.seen.count("attention") == 4
+    assert torch.isfinite(x).all()
