@@ -267,6 +267,79 @@ def measure_prefix(dev, layers=4, reps=5):
     return out
 
 
+def measure_groot(dev, reps=5):
+    """The GR00T N1.7 action head end to end on these kernels (instinctflash_amd/
+    groot.py; reference engines/groot_n17/engine.py:92-200): LayerNorm + 4 VLSA
+    blocks over 256 backbone rows, the 16 cross K/V projections, and 4 flow
+    steps of the 32-block DiT over 41 rows (the C2 MLP in every block), random
+    weights of the architecture, one captured graph; ms per inference."""
+    import torch
+    from instinctflash_amd.groot import ACT_DIM, HORIZON, VL_D, GrootHead, random_groot_weights
+    w = random_groot_weights(dev, seed=0)
+    head = GrootHead(w, dev, max_seq=256)
+    g = torch.Generator().manual_seed(1)
+    n = 256
+    head.set_inputs(torch.randn(n, VL_D, generator=g).to(dev), (torch.rand(n, generator=g) < 0.7).to(dev),
+                    torch.ones(n, dtype=torch.bool, device=dev), torch.randn(ACT_DIM, generator=g).to(dev),
+                    torch.randn(HORIZON, ACT_DIM, generator=g).to(dev))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        head.forward(n)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = capture(lambda i: head.forward(n), 1, side)
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    _log(f"[bench] GR00T N1.7 head: {ms:.3f} ms per inference")
+    out = {"workload": "GR00T N1.7 action head: 4 VLSA blocks x 256 rows, 16 cross K/V, 4 steps x 32 DiT blocks "
+                       "x 41 rows (random weights)", "ms_per_inference": round(ms, 4)}
+    del head, w, graph
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_wan(dev, blocks=4, reps=5):
+    """The LingBot-VA (Wan2.2 5B) transformer blocks on these kernels
+    (instinctflash_amd/wan_block.py; reference engines/wan_va/engine.py:
+    205-245) at the engine's largest forward (2 batches x 512 tokens, 1024 rows
+    of the C5 projections) over a 4096-slot KV pool with 2560 live slots and 512
+    text rows: `blocks` blocks captured in one graph; µs per block and its FP8
+    GEMM TFLOP/s."""
+    import torch
+    from instinctflash_amd.wan_block import WanStack, random_wan_blocks
+    B, T, S, live = 2, 512, 4096, 2560
+    st = WanStack(random_wan_blocks(blocks, dev, seed=0), dev, pool_slots=S, max_tokens=T, max_batch=B)
+    g = torch.Generator().manual_seed(1)
+    D, FF = st.D, st.FF
+    st.live[:live].copy_(torch.arange(live, dtype=torch.int32))
+    st.n_live.fill_(live)
+    st.slots[:T].copy_(torch.arange(live - T, live, dtype=torch.int32))
+    st.pos[:T].copy_(torch.stack([torch.arange(T) // 256, (torch.arange(T) // 16) % 16, torch.arange(T) % 16], 1))
+    st.mod_index.copy_((torch.randint(0, 2, (B * T,), generator=g) * 6).int())
+    block_mod = (torch.randn(blocks, 2, 6, D, generator=g) * 0.1).to(dev)
+    head_mod = (torch.randn(2, 6, D, generator=g) * 0.1).to(dev)
+    st.prepare_text(torch.randn(B, st.TEXT, D, generator=g).to(dev))
+    x = torch.randn(B * T, D, generator=g).to(dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st.forward(B, T, block_mod, head_mod, x=x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = capture(lambda i: st.forward(B, T, block_mod, head_mod, x=x), 1, side)
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    us = ms * 1e3 / blocks
+    R = B * T
+    flops = 2 * R * D * (3 * D + D + D + D + 2 * FF)  # qkv, o, cross q, cross o, ff1, ff2
+    _log(f"[bench] Wan blocks: {us:.1f} us per block ({flops / us / 1e6:.0f} TFLOP/s of FP8 GEMM)")
+    out = {"workload": f"LingBot-VA Wan2.2 5B blocks, {B} x {T} tokens, {live} live pool slots, 512 text rows "
+                       "(random weights)", "blocks": blocks, "us_per_block": round(us, 2),
+           "gemm_tflops": round(flops / us / 1e6, 1)}
+    del st, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -488,6 +561,8 @@ def main():
         out["producers"] = measure_producers(dev)
         out["engine"] = measure_engine(dev)
         out["prefix"] = measure_prefix(dev)
+        out["groot"] = measure_groot(dev)
+        out["wan"] = measure_wan(dev)
     if not args.no_cpu:
         for key in order:
             _log(f"[bench] CPU baseline {key} (reference CPU FP8 path)")
