@@ -155,9 +155,11 @@ def test_large_m_epilogue_combinations(gpu, oracle_mod, act, res, gate):
                                        (4112, 12304, 384, None), (3000, 16416, 640, "geglu"),
                                        (2100, 24608, 128, "swiglu"), (8192, 6144, 1024, "gelu_tanh"),
                                        (8100, 3056, 128, None), (7900, 3040, 256, "gelu_tanh"),
-                                       (5000, 3840, 384, None), (8192, 3072, 640, None)])
+                                       (5000, 3840, 384, None), (8192, 3072, 640, None),
+                                       (1000, 22016, 256, "swiglu"), (777, 21952, 128, "geglu")])
 def test_wide_tile_k_loop_edges(gpu, oracle_mod, M, N, K, act):
-    # >= 192 tiles of 256 x 256 (or of 256 x 192 for the last four shapes): the
+    # >= 192 tiles of 256 x 256 (or of 256 x 192 for the last six shapes, the
+    # last two GLU with 4-row epilogue passes of 12-lane groups): the
     # 4-wave register-pipelined kernel, whose K
     # loop has a prologue of two stages, a main part that issues the stage two
     # ahead and a tail of up to two stages without DMA; K of 1..5 stages and
