@@ -267,6 +267,39 @@ def measure_prefix(dev, layers=4, reps=5):
     return out
 
 
+def measure_pi05_full(dev, reps=5):
+    """The whole pi05 forward on these kernels (instinctflash_amd/pi05_engine.py;
+    reference engines/pi05/engine.py:151-245): 3 camera views through the
+    27-layer SigLIP tower and the projector, the 18-layer Gemma-2B prefix over
+    816 rows (768 image + 48 prompt rows: config C3's M), and 10 Euler steps of
+    the 18-layer action expert, one captured graph, random weights; ms per
+    50-action chunk (the reference publishes 51.85 ms for this forward on
+    Jetson Thor, README.md:38)."""
+    import torch
+    from instinctflash_amd.pi05_engine import LM_D, Pi05Engine, random_pi05_weights
+    w = random_pi05_weights(dev, seed=0)
+    eng = Pi05Engine(w, 3, dev, max_prompt=48)
+    g = torch.Generator().manual_seed(1)
+    eng.img.copy_(torch.rand(3, 3, 224, 224, generator=g) * 2 - 1)
+    eng.expert.noise.copy_(torch.randn(eng.expert.chunk, 32, generator=g))
+    M = eng.set_prompt(torch.randn(48, LM_D, generator=g).to(dev))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eng.forward(M)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = capture(lambda i: eng.forward(M), 1, side)
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    _log(f"[bench] pi05 full forward: {ms:.3f} ms per chunk (3 views, {M} prefix rows)")
+    out = {"workload": "pi05: 3 views x SigLIP 27 layers, Gemma-2B prefix 18 layers x 816 rows, expert 10 steps x 18 "
+                       "layers, chunk 50 (random weights)", "ms_per_chunk": round(ms, 3),
+           "reference_published_ms": {"value": 51.85, "hardware": "Jetson Thor", "source": "README.md:38"}}
+    del eng, w, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_groot(dev, reps=5):
     """The GR00T N1.7 action head end to end on these kernels (instinctflash_amd/
     groot.py; reference engines/groot_n17/engine.py:92-200): LayerNorm + 4 VLSA
@@ -561,6 +594,7 @@ def main():
         out["producers"] = measure_producers(dev)
         out["engine"] = measure_engine(dev)
         out["prefix"] = measure_prefix(dev)
+        out["pi05_full"] = measure_pi05_full(dev)
         out["groot"] = measure_groot(dev)
         out["wan"] = measure_wan(dev)
     if not args.no_cpu:
