@@ -300,6 +300,39 @@ def measure_pi05_full(dev, reps=5):
     return out
 
 
+def measure_vla4_full(dev, reps=5):
+    """The LingBot-VLA-4B forward on these kernels (instinctflash_amd/
+    vla4_engine.py; reference engines/vla4/engine.py:109-177): the 36-layer
+    Qwen2.5 prefix over 192 vision + 48 prompt rows and 10 Euler steps of the
+    36-layer expert over the 51 suffix rows, one captured graph, random weights;
+    ms per 50-action chunk (the vision embeddings are an input, as upstream,
+    where the model's own bf16 tower makes them)."""
+    import torch
+    from instinctflash_amd.vla4_engine import D, STATE_DIM, VISION_TOKENS, Vla4Engine, random_vla4_weights
+    eng = Vla4Engine(random_vla4_weights(dev, seed=0), dev)
+    g = torch.Generator().manual_seed(1)
+    eng.vis.copy_(torch.randn(VISION_TOKENS, D, generator=g))
+    eng.state.copy_(torch.randn(1, STATE_DIM, generator=g))
+    eng.noise.copy_(torch.randn(eng.chunk, STATE_DIM, generator=g))
+    M = eng.set_prompt(torch.randn(48, D, generator=g).to(dev))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eng.forward(M)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = capture(lambda i: eng.forward(M), 1, side)
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    _log(f"[bench] LingBot-VLA-4B forward: {ms:.3f} ms per chunk ({M} prefix rows)")
+    out = {"workload": "LingBot-VLA-4B: Qwen2.5 prefix 36 layers x 240 rows, expert 10 steps x 36 layers x 51 rows "
+                       "(random weights; vision embeddings as input)", "ms_per_chunk": round(ms, 3),
+           "reference_published_ms": {"value": 221.53, "hardware": "Jetson Thor", "source": "README.md:34",
+                                      "note": "whole prediction, bf16 vision tower included"}}
+    del eng, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_groot(dev, reps=5):
     """The GR00T N1.7 action head end to end on these kernels (instinctflash_amd/
     groot.py; reference engines/groot_n17/engine.py:92-200): LayerNorm + 4 VLSA
@@ -595,6 +628,7 @@ def main():
         out["engine"] = measure_engine(dev)
         out["prefix"] = measure_prefix(dev)
         out["pi05_full"] = measure_pi05_full(dev)
+        out["vla4_full"] = measure_vla4_full(dev)
         out["groot"] = measure_groot(dev)
         out["wan"] = measure_wan(dev)
     if not args.no_cpu:

@@ -1,0 +1,148 @@
+"""The LingBot-VLA-4B forward (Qwen2.5 prefix + flow-matching expert) on the
+gfx950 kernels, reference instinctflash/engines/vla4/engine.py
+(instinctflash_amd/vla4_engine.py). Reduced depth (3 layers, 2 Euler steps) at
+full width:
+
+  * every expert call against the oracle on the inputs it received: AdaRMSNorm
+    residuals bit-exact (float32) and FP8 rows within the reference test's bar
+    (7% of the row max, tests/test_gi_kernels.py:112), the final weight-form
+    RMSNorm's y within 1e-5; GEMMs at the north-star bar; the QKV split (+ bias,
+    rotary at the suffix positions) into the cache rows after the prefix at the
+    rope tests' fp16 bar; attention over the prefix K/V plus the suffix with the
+    state row seeing the prefix and itself (kv_extra) at 2e-3; SwiGLU
+    requantization at the quantizer tests' bar (reference calls) or bit-exact
+    (GLU epilogue + quant_rows). The prefix calls are the kernels checked call
+    by call in test_gpu_prefix.py (VLA4's C4 stack);
+  * the reference call sequence against the default layout;
+  * one captured graph replays the eager forward bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _u8(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _engine(gpu, seed, reference_calls=False):
+    from instinctflash_amd.vla4_engine import D, STATE_DIM, VISION_TOKENS, Vla4Engine, random_vla4_weights
+    w = random_vla4_weights(gpu, layers=3, steps=2, seed=seed)
+    eng = Vla4Engine(w, gpu, reference_calls=reference_calls)
+    g = torch.Generator().manual_seed(seed + 1)
+    eng.vis.copy_(torch.randn(VISION_TOKENS, D, generator=g))
+    eng.state.copy_(torch.randn(1, STATE_DIM, generator=g))
+    eng.noise.copy_(torch.randn(eng.chunk, STATE_DIM, generator=g))
+    return eng, torch.randn(72, D, generator=g)
+
+
+class ExpertChecker:
+    def __init__(self, oracle, eng):
+        self.o, self.eng, self.pre, self.seen = oracle, eng, None, []
+
+    def __call__(self, name, **t):
+        from instinctflash_amd.vla4_engine import HD, HKV, HQ
+        torch.cuda.synchronize()
+        o, eng = self.o, self.eng
+        S, P = eng.S, int(eng.prefix_len.item())
+        self.seen.append(name)
+        if name == "pre_res":
+            self.pre = _f(t["res"])
+        elif name == "norm":
+            kw = {}
+            if "mod" in t:
+                kw.update(mod_scale=_f(t["mod"][0]), mod_shift=_f(t["mod"][1]))
+            if "weight" in t:
+                kw["weight"] = _f(t["weight"])
+            if "delta" in t:
+                kw.update(delta=_f(t["delta"]), delta_row=_f(t["delta_row"]), delta_col=_f(t["w"].scale))
+            x_ref, y_ref = o.residual_norm(self.pre, **kw)
+            assert np.array_equal(_f(t["res"]).view(np.uint32), x_ref.view(np.uint32)), "residual not bit-exact"
+            if "q" in t:
+                deq = o.e4m3_decode(_u8(t["q"])) * _f(t["s"])[:, None]
+                assert (np.abs(deq - y_ref).max(axis=1) / np.abs(y_ref).max(axis=1)).max() < 0.07
+            else:
+                err = (np.abs(_f(t["y"]) - y_ref).max(axis=1) / np.abs(y_ref).max(axis=1)).max()
+                assert err <= 1e-5, f"y rel err {err:.3e}"
+        elif name in ("gemm", "swiglu"):
+            sa = t.get("sa")
+            w = t["w"]
+            ref = o.ref_linear(_u8(t["a"]), None if sa is None else _f(sa), _u8(w.w),
+                               None if sa is None else _f(w.scale), act="swiglu" if name == "swiglu" else None)
+            got = _f(t["out"])
+            _, cos = o.parity_stats(got, ref)
+            rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+            excess = np.abs(got - ref) - (2e-2 * rms + 2.0 ** -8 * np.abs(ref))
+            assert excess.max() <= 0 and cos >= 0.9999, f"{name} {tuple(w.w.shape)}: {excess.max():.3e} {cos:.7f}"
+        elif name == "qkv_split":
+            w = t["w"]
+            q, k, v = o.qkv_split(_f(t["raw"]), HQ, HKV, HD, row=_f(t["row"]), col=_f(w.scale), bias=_f(w.bias),
+                                  inv_freq=_f(eng.inv_freq), pos=_f(eng.pos_suffix))
+            for nm, got, ref in (("q", t["q"], q), ("k", t["k"][P:P + S], k), ("v", t["v"][P:P + S], v)):
+                err = np.abs(_f(got).astype(np.float64) - ref) - (2.0 ** -10 * np.abs(ref) + 2e-5)
+                assert err.max() <= 0, f"qkv_split {nm}: excess {err.max():.3e}"
+        elif name == "attention":
+            limits = P + _f(eng.kv_extra).astype(np.int64)
+            n = P + S
+            ref = o.attention(_f(t["q"]), _f(t["k"][:, :n]), _f(t["v"][:, :n]), limits, HD ** -0.5)
+            err = np.abs(_f(t["out"]) - ref).max()
+            assert err < 2e-3, f"attention: max |d| {err:.3e}"
+        elif name == "row_quant":
+            x = t["x"]
+            eq, es = o.quant_rows(_bits(x) if x.dtype == torch.bfloat16 else _f(x))
+            assert np.array_equal(_u8(t["q"]), eq) and np.array_equal(_f(t["s"]).view(np.uint32), es.view(np.uint32))
+        elif name == "gated_act_quant":
+            F = t["gu"].shape[1] // 2
+            x = _f(t["gu"]) * _f(t["row"])[:, None] * _f(t["w"].scale)[None, :]
+            h = o.silu(x[:, :F].astype(np.float32)) * x[:, F:].astype(np.float32)
+            eq, es = o.quant_rows(h.astype(np.float32))
+            s = _f(t["s"])
+            assert np.all(np.abs(s.view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
+            assert (_u8(t["q"]) == eq).mean() > 0.999
+        else:
+            raise AssertionError(f"unchecked call {name}")
+
+
+@pytest.mark.parametrize("reference_calls", [False, True])
+def test_expert_calls_against_oracle(gpu, oracle_mod, reference_calls):
+    eng, lang = _engine(gpu, seed=2, reference_calls=reference_calls)
+    M = eng.set_prompt(lang[:40])
+    print(f"[vla4 engine] rows={M} reference_calls={reference_calls}", flush=True)
+    chk = ExpertChecker(oracle_mod, eng)
+    x = eng.forward(M, on_call=chk)
+    assert chk.seen.count("attention") == 3 * 2 and torch.isfinite(x).all()
+
+
+def test_reference_calls_agree_and_graph(gpu):
+    a_eng, lang = _engine(gpu, seed=4, reference_calls=True)
+    b_eng, _ = _engine(gpu, seed=4)
+    M = a_eng.set_prompt(lang[:40])
+    b_eng.set_prompt(lang[:40])
+    a = a_eng.forward(M).clone()
+    b = b_eng.forward(M).clone()
+    cos = float(torch.nn.functional.cosine_similarity(a.flatten().double(), b.flatten().double(), dim=0))
+    assert cos > 0.999, cos
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        b_eng.forward(M)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        b_eng.forward(M)
+    for _ in range(2):
+        b_eng.x_t.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(b_eng.x_t, b), "replay differs from the eager forward"
+        a_eng.forward(M)  # eager work between replays
