@@ -189,3 +189,41 @@ def test_many_splits_long_keys(gpu, oracle_mod, dtype):
     ws = SplitWorkspace(1, 33, 8, 1, 256, 16, gpu)
     out = attention(q.to(gpu), k.to(gpu), v.to(gpu), kv_len=n, split=ws)
     _close(out, _ref(oracle_mod, q, k, v, np.full(33, 3900)), dtype, f"16 splits {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_split_partials_q8_agreement(gpu, oracle_mod, dtype):
+    # The split partial rows are stored normalized in the operands' 16-bit type
+    # (the reference keeps fp32 partials, kernels/attention.py:155). What that costs
+    # the fused e4m3 row, at the pi05 chunk's shape (51 queries over 851 keys, 8/1
+    # heads of 256, 14 splits), against the oracle recipe applied to the exact
+    # float64 attention rows -- measured: fp16 1.27% of the codes differ, scale drift
+    # 3.1e-4; bf16 7.2% and 2.3e-3; codes more than one step apart (or of opposite
+    # sign) only where a value is below 2.2e-3 / 1.6e-2 of its row max; the
+    # dequantized rows stay within 3.7% of the row max. Bounds: the reference
+    # test's 7% row bar (tests/test_gi_kernels.py:112), differing codes <= 2% / 10%,
+    # scale drift <= 2^-11 / 2^-8 (fp16 / bf16), far codes only below 1/32 of the
+    # row max
+    from instinctflash_amd.kernels import SplitWorkspace, attention
+    T, hq, hd = 51, 8, 256
+    q, k, v = _qkv(1, T, 851, hq, 1, hd, 77, dtype)
+    n = torch.tensor([851], device=gpu, dtype=torch.int32)
+    ws = SplitWorkspace(1, T, hq, 1, hd, 14, gpu)
+    q8 = torch.empty(T, hq * hd, device=gpu, dtype=torch.float8_e4m3fn)
+    qs = torch.empty(T, device=gpu)
+    attention(q.to(gpu), k.to(gpu), v.to(gpu), kv_len=n, split=ws, q8=q8, q8_scale=qs)
+    r = _ref(oracle_mod, q, k, v, np.full(T, 851)).reshape(T, -1).astype(np.float32)
+    eq, es = oracle_mod.quant_rows(r)
+    got = q8.view(torch.uint8).cpu().numpy()
+    differ = (got != eq).mean()
+    drift = np.abs(qs.cpu().numpy() / es - 1).max()
+    deq = oracle_mod.e4m3_decode(got) * qs.cpu().numpy()[:, None]
+    rowmax = np.abs(r).max(axis=1, keepdims=True)
+    rel = (np.abs(deq - r) / rowmax).max()
+    # codes more than one step apart: values small against their row max
+    far = (np.abs(got.astype(np.int16) - eq.astype(np.int16)) > 1) | ((got & 0x80) != (eq & 0x80))
+    small = (np.abs(r) / rowmax)[far].max() if far.any() else 0.0
+    print(f"[attn q8 {dtype}] differing codes {differ:.4%}, scale drift {drift:.2e}, err / row max {rel:.3e}, "
+          f"largest |value| / row max among far codes {small:.3e}", flush=True)
+    bound = {torch.float16: (0.02, 2.0 ** -11), torch.bfloat16: (0.10, 2.0 ** -8)}[dtype]
+    assert rel < 0.07 and differ <= bound[0] and drift <= bound[1] and small < 1 / 32, (rel, differ, drift, small)
