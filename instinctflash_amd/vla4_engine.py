@@ -17,10 +17,14 @@ Mirrors instinctflash/engines/vla4/engine.py:
     SwiGLU requantization, down, residual + the next AdaRMSNorm or the final
     weight-form RMSNorm (float32 ``y``), then the Euler update.
 
-``reference_calls=True`` makes exactly the reference's calls; the default applies
-SwiGLU in the gate|up projections' epilogues (GLU-packed weights, half-width
-bf16) and requantizes that with ``quant_rows``. Weights are random with the
-published shapes (no checkpoint here).
+``reference_calls=True`` makes exactly the reference's calls. The default lays
+the same math out for gfx950: SwiGLU in the gate|up projections' epilogues
+(GLU-packed weights, half-width bf16, requantized with ``quant_rows`` /
+``row_quant``), and in the expert (51 rows) the pi05 expert's forms: weights in
+the skinny tile layout, every FP8 activation written by its producer in that
+layout, the QKV split in the QKV projection's epilogue (``linear_qkv_rope``) and
+the attention's split-KV combine emitting the o projection's FP8 operand.
+Weights are random with the published shapes (no checkpoint here).
 """
 from __future__ import annotations
 
@@ -28,9 +32,11 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels import E4M3, Fp8Weight, attention, gated_act_quant, gemm, linear, pack_glu, quant_rows, \
-    quantize_weight, qkv_split, residual_norm_quant, rope_inv_freq, row_quant
+from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, gated_act_quant, gemm, linear, \
+    linear_qkv_rope, pack_glu, pack_skinny, permute_rope_rows, quant_rows, quantize_weight, qkv_split, \
+    residual_norm_quant, rope_inv_freq, row_quant
 from .kernels.activation import SILU
+from .kernels.attention import split_count
 
 #: engines/vla4/engine.py:23-27
 VISION_TOKENS = 192
@@ -147,6 +153,17 @@ class Vla4Engine:
         self.ex = [glu(L) for L in weights.expert]
         self.h = torch.zeros(rows * FF, dtype=bf16, device=dev)
         self.rows = None
+        if not self.reference_calls:
+            from . import _lib
+            lib = _lib.load()
+            S = self.S
+            tiled = lambda k: TiledRows(torch.zeros(lib.ifx_quant_rows_tiled_bytes(S, k), dtype=E4M3,  # noqa: E731
+                                                    device=dev), S, k)
+            self.xq, self.oq, self.hq = tiled(EX_D), tiled(HQ * HD), tiled(EX_FF)
+            self.ex_tiled = [Layer(pack_skinny(permute_rope_rows(L.qkv, HQ, HKV, HD)), pack_skinny(L.o),
+                                   pack_skinny(pack_glu(L.gate_up)), pack_skinny(L.down)) for L in weights.expert]
+            splits = max(2, split_count(1, S, HQ, HKV, self.smax + S))
+            self.split = SplitWorkspace(1, S, HQ, HKV, HD, splits, dev)
 
     def q8(self, rows, cols):
         return self.q8buf[: rows * cols].view(rows, cols)
@@ -172,9 +189,14 @@ class Vla4Engine:
         M = self.rows if M is None else int(M)
         if M is None or not VISION_TOKENS < M <= self.smax:
             raise ValueError("set_prompt first (or M out of range)")
+        if on_call is not None and not self.reference_calls:
+            raise ValueError("on_call needs reference_calls=True")
         note = on_call or (lambda name, **t: None)
         self.prefix(M)
-        self.expert(note)
+        if self.reference_calls:
+            self.expert(note)
+        else:
+            self.expert_tiled()
         return self.x_t
 
     def _mlp(self, note, L, rows, width, ff, x_s, ref=None):
@@ -271,4 +293,39 @@ class Vla4Engine:
                                         weight=w.final_norm, y=self.dy)
                     note("norm", res=self.dx, delta=raw(S, EX_D), delta_row=s[1], w=L.down, weight=w.final_norm,
                          y=self.dy)
+            self.x_t.addmm_(self.dy[1:], self.out_w_dt).add_(self.out_b_dt)
+
+    def expert_tiled(self):
+        """The expert in the gfx950 layout (same math as ``expert``)."""
+        w, raw, S = self.w, self.raw, self.S
+        s = [v[:S] for v in self.scale]
+        xq, oq, hq = self.xq, self.oq, self.hq
+        torch.addmm(w.state_b, self.state, self.state_w_t, out=self.state_emb)
+        self.x_t.copy_(self.noise)
+        qv = self.q16[:S].view(1, S, HQ, HD)
+        last = len(self.ex_tiled) - 1
+        for step in range(w.steps):
+            ma, mf = w.mod_attn[step], w.mod_ffn[step]
+            self.dx[:1].copy_(self.state_emb)
+            torch.addmm(w.act_c[step], self.x_t, self.act_w_t, out=self.hid)
+            torch.nn.functional.silu(self.hid, inplace=True)
+            torch.addmm(w.mlp_out_b, self.hid, self.mlp_out_w_t, out=self.dx[1:])
+            residual_norm_quant(self.dx, mod_scale=ma[0, 0], mod_shift=ma[0, 1], q=xq, q_scale=s[0])
+            for i, L in enumerate(self.ex_tiled):
+                linear_qkv_rope(xq, s[0], L.qkv, self.q16[:S], self.kc[i], self.vc[i], inv_freq=self.inv_freq,
+                                pos=self.pos_suffix, kv_base=self.prefix_len)
+                attention(qv, self.kc[i][None], self.vc[i][None], kv_len=self.prefix_len, kv_extra=self.kv_extra,
+                          max_extra=S, split=self.split, q8=oq, q8_scale=s[1])
+                gemm(oq, L.o, raw(S, EX_D))
+                residual_norm_quant(self.dx, delta=raw(S, EX_D), delta_row=s[1], delta_col=L.o.scale,
+                                    mod_scale=mf[i, 0], mod_shift=mf[i, 1], q=xq, q_scale=s[0])
+                linear(xq, s[0], L.gate_up, out=raw(S, EX_FF), act="swiglu")
+                row_quant(raw(S, EX_FF), hq, s[1])
+                gemm(hq, L.down, raw(S, EX_D))
+                if i < last:
+                    residual_norm_quant(self.dx, delta=raw(S, EX_D), delta_row=s[1], delta_col=L.down.scale,
+                                        mod_scale=ma[i + 1, 0], mod_shift=ma[i + 1, 1], q=xq, q_scale=s[0])
+                else:
+                    residual_norm_quant(self.dx, delta=raw(S, EX_D), delta_row=s[1], delta_col=L.down.scale,
+                                        weight=w.final_norm, y=self.dy)
             self.x_t.addmm_(self.dy[1:], self.out_w_dt).add_(self.out_b_dt)
