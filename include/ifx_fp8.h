@@ -63,7 +63,7 @@ extern "C" {
  *        width N/2; see ifx_fp8_pack_glu)
  *   y = y * gate[n]                                  IFX_EPI_GATE   (adaLN gate, bf16 [N_out])
  *   y = residual[m,n] + y                            IFX_EPI_RESIDUAL
- *   out[m,n] = round(y)                              bf16, or f32 with IFX_EPI_OUT_F32
+ *   out[m,n] = round(y)                              bf16; f32 with IFX_EPI_OUT_F32, fp16 with IFX_EPI_OUT_F16
  * residual is bf16 unless IFX_EPI_RES_F32. out may alias residual (in-place update).
  * IFX_EPI_SCALAR_SA / IFX_EPI_SCALAR_SW: sa / sw point to ONE f32 shared by all
  * tokens / weight rows (per-tensor scales, reference runtime/torch_fp8_linear.py:75-78).
@@ -85,6 +85,8 @@ extern "C" {
 /* a is in the skinny tile layout written by ifx_quant_rows_tiled (M <= 64 only;
  * lda is ignored). */
 #define IFX_EPI_A_TILED 2048
+/* out is fp16 (the attention operands of the GR00T / SigLIP engines; not with IFX_EPI_OUT_F32). */
+#define IFX_EPI_OUT_F16 4096
 
 int ifx_abi_version(void);
 /* Host pointer to a static string describing a status code. */

@@ -50,6 +50,7 @@ EPI_SCALAR_SA = 256
 EPI_SCALAR_SW = 512
 EPI_W_TILED = 1024
 EPI_A_TILED = 2048
+EPI_OUT_F16 = 4096
 RNQ_WRITE_RES = 1
 RNQ_LAYERNORM = 2
 SCALE_ROW = 0

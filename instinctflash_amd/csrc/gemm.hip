@@ -88,6 +88,8 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
   return a * b;
 }
 
+__device__ __forceinline__ void epi_store4(const Epi& e, int64_t m, int64_t c, const float* y);
+
 // y (four consecutive output columns c..c+3 of row m, after activation) ->
 // gate, residual, store.
 __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, float* y) {
@@ -110,14 +112,7 @@ __device__ __forceinline__ void epi_finish4(const Epi& e, int64_t m, int64_t c, 
       y[3] += __uint_as_float(r.y & 0xFFFF0000u);
     }
   }
-  if (e.flags & IFX_EPI_OUT_F32) {
-    *reinterpret_cast<float4*>(static_cast<float*>(e.out) + m * e.ldo + c) = make_float4(y[0], y[1], y[2], y[3]);
-  } else {
-    uint2 o;
-    o.x = pack_bf16x2(y[0], y[1]);
-    o.y = pack_bf16x2(y[2], y[3]);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.out) + m * e.ldo + c) = o;
-  }
+  epi_store4(e, m, c, y);
 }
 
 // First half of the epilogue for one lane's D fragment (weight rows n..n+3,
@@ -136,10 +131,16 @@ __device__ __forceinline__ void epi_pre(const Epi& e, const v4f acc, int64_t n, 
   }
 }
 
-// Store four finished values at out[m, c..c+3] (bf16, or f32 with IFX_EPI_OUT_F32).
+// Store four finished values at out[m, c..c+3] (bf16; f32 with IFX_EPI_OUT_F32,
+// fp16 with IFX_EPI_OUT_F16).
 __device__ __forceinline__ void epi_store4(const Epi& e, int64_t m, int64_t c, const float* y) {
   if (e.flags & IFX_EPI_OUT_F32) {
     *reinterpret_cast<float4*>(static_cast<float*>(e.out) + m * e.ldo + c) = make_float4(y[0], y[1], y[2], y[3]);
+  } else if (e.flags & IFX_EPI_OUT_F16) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = {static_cast<_Float16>(y[0]), static_cast<_Float16>(y[1]), static_cast<_Float16>(y[2]),
+                  static_cast<_Float16>(y[3])};
+    *reinterpret_cast<h4*>(static_cast<_Float16*>(e.out) + m * e.ldo + c) = h;
   } else {
     uint2 o;
     o.x = pack_bf16x2(y[0], y[1]);
@@ -870,7 +871,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
   };
   const int fl = e.flags;
-  const bool plain_io = !(fl & (IFX_EPI_OUT_F32 | IFX_EPI_RES_F32));
+  const bool plain_io = !(fl & (IFX_EPI_OUT_F32 | IFX_EPI_OUT_F16 | IFX_EPI_RES_F32));
   const int gr = ((fl & IFX_EPI_GATE) ? 4 : 0) | ((fl & IFX_EPI_RESIDUAL) ? 8 : 0);
   using std::integral_constant;
   if constexpr (GLU) {
@@ -1504,8 +1505,10 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
                  const void* gate, int epilogue, const void* out, int64_t ldo, int64_t M, int64_t N, int64_t K) {
   constexpr int kKnown = IFX_EPI_BIAS | IFX_EPI_GELU_TANH | IFX_EPI_GEGLU | IFX_EPI_SWIGLU |
                          IFX_EPI_RESIDUAL | IFX_EPI_GATE | IFX_EPI_OUT_F32 | IFX_EPI_RES_F32 |
-                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW | IFX_EPI_W_TILED | IFX_EPI_A_TILED;
+                         IFX_EPI_SCALAR_SA | IFX_EPI_SCALAR_SW | IFX_EPI_W_TILED | IFX_EPI_A_TILED |
+                         IFX_EPI_OUT_F16;
   if (epilogue & ~kKnown) return IFX_ERR_INVALID;
+  if ((epilogue & IFX_EPI_OUT_F32) && (epilogue & IFX_EPI_OUT_F16)) return IFX_ERR_INVALID;
   const bool glu = (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0;
   const bool tiled = (epilogue & IFX_EPI_W_TILED) != 0;
   // the tile layouts serve M <= 64

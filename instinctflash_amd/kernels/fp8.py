@@ -286,8 +286,10 @@ def _epilogue(M, K, device, w: Fp8Weight, out, flags, residual, gate, use_scales
     n_out = N // 2 if glu else N
     if out.dtype == torch.float32:
         flags |= _lib.EPI_OUT_F32
+    elif out.dtype == torch.float16:
+        flags |= _lib.EPI_OUT_F16
     elif out.dtype != torch.bfloat16:
-        raise ValueError(f"out must be bf16 or fp32, got {out.dtype}")
+        raise ValueError(f"out must be bf16, fp16 or fp32, got {out.dtype}")
     Mo, _, ldo = _rows("out", out, out.dtype, device, cols=n_out)
     if Mo != M:
         raise ValueError(f"out has {Mo} rows, expected {M}")

@@ -85,8 +85,11 @@ def test_contract_violations_rejected_before_launch(lib):
     # GeGLU and SwiGLU together, unknown flag
     assert lib.ifx_fp8_linear(fake, 64, None, fake, 64, None, None, None, 0, None,
                               _lib.EPI_GEGLU | _lib.EPI_SWIGLU, fake, 32, 16, 64, 64, None, 0, None) == _lib.ERR_INVALID
-    assert lib.ifx_fp8_linear(fake, 64, None, fake, 64, None, None, None, 0, None, 1 << 12, fake, 64,
+    assert lib.ifx_fp8_linear(fake, 64, None, fake, 64, None, None, None, 0, None, 1 << 13, fake, 64,
                               16, 64, 64, None, 0, None) == _lib.ERR_INVALID
+    # fp16 and fp32 output together
+    assert lib.ifx_fp8_linear(fake, 64, None, fake, 64, None, None, None, 0, None,
+                              _lib.EPI_OUT_F16 | _lib.EPI_OUT_F32, fake, 64, 16, 64, 64, None, 0, None) == _lib.ERR_INVALID
     # misaligned operand pointer
     assert lib.ifx_fp8_linear(P(0x1001), 64, None, fake, 64, None, None, None, 0, None, 0, fake, 64,
                               16, 64, 64, None, 0, None) == _lib.ERR_ALIGN

@@ -55,7 +55,7 @@ def _ref(oracle_mod, qa, sa, fw, **kw):
 
 
 def _check(gpu, oracle_mod, qa, sa, fw, what, ref_w=None, act=None, residual=None, gate=None):
-    """fp32-output arithmetic within tolerance + bf16 output == RNE(fp32 output)."""
+    """fp32-output arithmetic within tolerance + bf16 / fp16 outputs == RNE(fp32 output)."""
     from instinctflash_amd.kernels import linear
     r = None if residual is None else residual.to(gpu)
     gt = None if gate is None else gate.to(gpu)
@@ -66,6 +66,9 @@ def _check(gpu, oracle_mod, qa, sa, fw, what, ref_w=None, act=None, residual=Non
                gate=None if gate is None else gate.float().numpy())
     _assert_close(_f(o32), ref, what)
     assert torch.equal(o16.view(torch.int16), o32.to(torch.bfloat16).view(torch.int16)), f"{what}: bf16 store"
+    # the fp16 output mode (IFX_EPI_OUT_F16): the same fp32 values, RNE to fp16
+    oh = linear(qa, sa, fw, act=act, residual=r, gate=gt, out_dtype=torch.float16)
+    assert torch.equal(oh.view(torch.int16), o32.to(torch.float16).view(torch.int16)), f"{what}: fp16 store"
     return o32, o16
 
 
