@@ -16,9 +16,12 @@ Mirrors instinctflash/engines/groot_n17/engine.py:92-200:
     rows -- each with AdaLN-modulated LayerNorms, and the GELU MLP; after the last
     block the output modulation, the decoder and the Euler update of the actions.
 
-``reference_calls=True`` makes exactly the reference's calls. The default lays
-the MLPs out for gfx950: GELU in the ff1 projection's epilogue (bf16 result) and
-``quant_rows`` of it, instead of the raw accumulator and ``row_quant(gelu=True)``.
+``reference_calls=True`` makes exactly the reference's calls. The default lays the
+same math out for gfx950: the q|k|v and cross K/V projections write their
+rescaled fp16 rows from the GEMM epilogue (no raw accumulator, no
+``dequant_rows``), GELU is applied in the ff1 epilogue, and the DiT (41 rows)
+runs in the skinny tile layouts with the attention's split-KV combine writing the
+o projection's FP8 operand (7 kernels per block instead of 10).
 Weights are random (no checkpoint here) with the published shapes; the model is
 built with any number of VLSA / DiT blocks (the published head has 4 and 32).
 """
@@ -28,8 +31,9 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels import E4M3, Fp8Weight, attention, dequant_rows, gemm, linear, quant_rows, quantize_weight, \
-    residual_norm_quant, row_quant
+from .kernels import E4M3, Fp8Weight, SplitWorkspace, TiledRows, attention, dequant_rows, gemm, linear, \
+    pack_skinny, quant_rows, quantize_weight, residual_norm_quant, row_quant
+from .kernels.attention import split_count
 
 #: engines/groot_n17/engine.py:17-21
 VL_D, VL_H, VL_HD, VL_FF = 2048, 32, 64, 8192
@@ -156,13 +160,25 @@ class GrootHead:
         self.qkv16 = torch.zeros(rows, 3 * VL_D, dtype=f16, device=dev)
         self.o16 = torch.zeros(rows, VL_D, dtype=f16, device=dev)
         n_cross = sum(b.cross for b in weights.dit)
-        self.kc = torch.zeros(n_cross, S, H, HD, dtype=f16, device=dev)
-        self.vc = torch.zeros_like(self.kc)
+        # cross K and V of a block side by side per row ([..., 0, :, :] K, [..., 1, :, :] V),
+        # so one projection writes both
+        self.kv16 = torch.zeros(n_cross, S, 2, H, HD, dtype=f16, device=dev)
+        self.kc, self.vc = self.kv16[:, :, 0], self.kv16[:, :, 1]
         self.h = torch.zeros(SA, D, dtype=f32, device=dev)
         self.y = torch.zeros(SA, D, dtype=f32, device=dev)
         self.a_t = torch.zeros(HORIZON, ACT_DIM, dtype=f32, device=dev)
         self.state_emb = torch.zeros(1, D, dtype=f32, device=dev)
         self.enc_tmp = torch.zeros(1, 1024, dtype=f32, device=dev)
+        if not self.reference_calls:
+            from . import _lib
+            lib = _lib.load()
+            tiled = lambda k: TiledRows(torch.zeros(lib.ifx_quant_rows_tiled_bytes(SA, k), dtype=E4M3,  # noqa: E731
+                                                    device=dev), SA, k)
+            self.xq, self.oq, self.hq = tiled(D), tiled(D), tiled(FF)
+            self.dit_t = [DitBlock(b.cross, b.text, pack_skinny(b.qkv), b.kv, pack_skinny(b.o), pack_skinny(b.ff1),
+                                   pack_skinny(b.ff2)) for b in weights.dit]
+            self.split_self = SplitWorkspace(1, SA, H, H, HD, max(2, split_count(1, SA, H, H, SA)), dev)
+            self.split_cross = SplitWorkspace(1, SA, H, H, HD, max(2, split_count(1, SA, H, H, S)), dev)
 
     def q8(self, rows, cols):
         return self.q8buf[: rows * cols].view(rows, cols)
@@ -189,10 +205,15 @@ class GrootHead:
     def forward(self, M, on_call=None):
         if not 1 <= M <= self.max_seq:
             raise ValueError(f"M must be in [1, {self.max_seq}]")
+        if on_call is not None and not self.reference_calls:
+            raise ValueError("on_call needs reference_calls=True")
         note = on_call or (lambda name, **t: None)
         self.vlsa(M, note)
         self.cross_kv(M, note)
-        self.dit(note)
+        if self.reference_calls:
+            self.dit(note)
+        else:
+            self.dit_fused()
         return self.a_t
 
     def _mlp(self, note, x_q, x_s, blk, rows, width, ff):
@@ -228,10 +249,13 @@ class GrootHead:
         note("norm_vl", res=vx, weight=L0.ln1_w, beta=L0.ln1_b, q=q8(M, VL_D), s=s[0])
         view = (1, M, VL_H, VL_HD)
         for i, L in enumerate(w.vlsa):
-            gemm(q8(M, VL_D), L.qkv, raw(M, 3 * VL_D))
-            note("gemm", a=q8(M, VL_D), w=L.qkv, out=raw(M, 3 * VL_D))
-            dequant_rows(raw(M, 3 * VL_D), self.qkv16[:M], row=s[0], col=L.qkv.scale, bias=L.qkv.bias)
-            note("dequant", x=raw(M, 3 * VL_D), y=self.qkv16[:M], row=s[0], w=L.qkv)
+            if self.reference_calls:
+                gemm(q8(M, VL_D), L.qkv, raw(M, 3 * VL_D))
+                note("gemm", a=q8(M, VL_D), w=L.qkv, out=raw(M, 3 * VL_D))
+                dequant_rows(raw(M, 3 * VL_D), self.qkv16[:M], row=s[0], col=L.qkv.scale, bias=L.qkv.bias)
+                note("dequant", x=raw(M, 3 * VL_D), y=self.qkv16[:M], row=s[0], w=L.qkv)
+            else:
+                linear(q8(M, VL_D), s[0], L.qkv, out=self.qkv16[:M])
             qkv = self.qkv16[:M].view(1, M, 3, VL_H, VL_HD)
             ov = self.o16[:M].view(view)
             attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], out=ov, kv_len=self.seq_len)
@@ -282,9 +306,12 @@ class GrootHead:
             for i, blk in enumerate(self.w.dit):
                 if not blk.cross or blk.text != (key == "text"):
                     continue
+                ci = i // 2
+                if not self.reference_calls:
+                    linear(q8(M, VL_D), s0, blk.kv, out=self.kv16[ci, :M].view(M, 2 * D))
+                    continue
                 gemm(q8(M, VL_D), blk.kv, raw(M, 2 * D))
                 note("gemm", a=q8(M, VL_D), w=blk.kv, out=raw(M, 2 * D))
-                ci = i // 2
                 dequant_rows(raw(M, 2 * D)[:, :D], self.kc[ci, :M].view(M, D), row=s0, col=blk.kv.scale[:D],
                              bias=blk.kv.bias[:D])
                 dequant_rows(raw(M, 2 * D)[:, D:], self.vc[ci, :M].view(M, D), row=s0, col=blk.kv.scale[D:],
@@ -362,6 +389,60 @@ class GrootHead:
                                         y=self.y, eps=OUT_EPS)
                     note("norm_out", res=self.h, delta=raw(SA, D), delta_row=s[1], w=blk.ff2, mod=(om[1], om[0]),
                          y=self.y)
+            out = torch.addmm(w.proj_out_b, self.y[1:], w.proj_out_w)
+            v = torch.addmm(w.dec_b2, torch.relu(torch.addmm(w.dec_b1, out, w.dec_w1)), w.dec_w2)
+            self.a_t.add_(v, alpha=w.dt)
+
+    def dit_fused(self):
+        """``dit`` in the gfx950 layout (same math): tile-layout FP8 rows, fp16
+        q|k|v straight from the projection epilogue, the attention combine
+        writing the o projection's FP8 operand, GELU in the ff1 epilogue."""
+        w, raw = self.w, self.raw
+        s = [v[:SA] for v in self.scale]
+        xq, oq, hq = self.xq, self.oq, self.hq
+        torch.addmm(w.state_b1, self.state, w.state_w1, out=self.enc_tmp)
+        torch.relu_(self.enc_tmp)
+        torch.addmm(w.state_b2, self.enc_tmp, w.state_w2, out=self.state_emb)
+        self.a_t.copy_(self.noise)
+        view = (1, SA, H, HD)
+        qkv16 = self.qkv16[:SA]
+        last = len(self.dit_t) - 1
+        for step in range(w.steps):
+            mod = w.mod[step]
+            self.h[:1].copy_(self.state_emb)
+            act = torch.addmm(w.act_c[step], self.a_t, w.act_w)
+            act = act * torch.sigmoid(act)
+            torch.addmm(w.act_b3, act, w.act_w3, out=self.h[1:])
+            self.h[1:].add_(w.pos)
+            residual_norm_quant(self.h, layernorm=True, mod_scale=mod[0, 0], mod_shift=mod[0, 1], q=xq,
+                                q_scale=s[0], eps=LN_EPS)
+            for i, blk in enumerate(self.dit_t):
+                if blk.cross:
+                    linear(xq, s[0], blk.qkv, out=qkv16[:, :D])
+                    ci = i // 2
+                    attention(qkv16[:, :D].view(view), self.kc[ci][None], self.vc[ci][None],
+                              kv_len=self.n_txt if blk.text else self.n_img, split=self.split_cross, q8=oq,
+                              q8_scale=s[1])
+                else:
+                    linear(xq, s[0], blk.qkv, out=qkv16[:, :3 * D])
+                    qkv = qkv16[:, :3 * D].view(1, SA, 3, H, HD)
+                    attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], split=self.split_self, q8=oq, q8_scale=s[1])
+                gemm(oq, blk.o, raw(SA, D))
+                residual_norm_quant(self.h, delta=raw(SA, D), delta_row=s[1], delta_col=blk.o.scale, bias=blk.o.bias,
+                                    layernorm=True, q=xq, q_scale=s[0], eps=LN_EPS)
+                linear(xq, s[0], blk.ff1, out=raw(SA, FF), act="gelu_tanh")
+                row_quant(raw(SA, FF), hq, s[1])
+                gemm(hq, blk.ff2, raw(SA, D))
+                if i < last:
+                    nm = mod[i + 1]
+                    residual_norm_quant(self.h, delta=raw(SA, D), delta_row=s[1], delta_col=blk.ff2.scale,
+                                        bias=blk.ff2.bias, layernorm=True, mod_scale=nm[0], mod_shift=nm[1], q=xq,
+                                        q_scale=s[0], eps=LN_EPS)
+                else:
+                    om = w.out_mod[step]
+                    residual_norm_quant(self.h, delta=raw(SA, D), delta_row=s[1], delta_col=blk.ff2.scale,
+                                        bias=blk.ff2.bias, layernorm=True, mod_scale=om[1], mod_shift=om[0],
+                                        y=self.y, eps=OUT_EPS)
             out = torch.addmm(w.proj_out_b, self.y[1:], w.proj_out_w)
             v = torch.addmm(w.dec_b2, torch.relu(torch.addmm(w.dec_b1, out, w.dec_w1)), w.dec_w2)
             self.a_t.add_(v, alpha=w.dt)
