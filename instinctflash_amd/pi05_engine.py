@@ -4,11 +4,11 @@ prefix, Gemma-300M flow-matching expert, captured as one graph.
 Mirrors instinctflash/engines/pi05/engine.py:
   * ``vision`` (:157-190): the 14 x 14 patch embedding as one fp16 matmul over the
     reshaped pixels plus position embeddings (torch, as upstream), then per
-    SigLIP layer: LayerNorm to FP8, q|k|v projection, rescale + bias to fp16
-    (``dequant_rows``), attention over each view's 256 patches, FP8 of its
-    output, o projection, residual + LayerNorm, fc1 with GELU and
-    requantization, fc2, residual + the next LayerNorm (the post-LayerNorm after
-    the last layer); the projector into the prefix rows (``dequant_rows``);
+    SigLIP layer: LayerNorm to FP8, q|k|v projection, rescale + bias to fp16,
+    attention over each view's 256 patches, FP8 of its output, o projection,
+    residual + LayerNorm, fc1 with GELU and requantization, fc2, residual + the
+    next LayerNorm (the post-LayerNorm after the last layer); the projector into
+    the float32 prefix rows;
   * ``prefix`` (:192-216): the language rows after the image rows, RMS pre-norm
     to FP8, per layer q|k|v, QKV split with rotary into the K/V cache, attention
     up to the device-side prefix length, o projection, residual + pre-norm,
@@ -19,9 +19,11 @@ Mirrors instinctflash/engines/pi05/engine.py:
 
 The prompt length lives in device memory (``set_prompt``), so one captured graph
 per physical row count serves every prompt of that bucket. ``reference_calls``
-selects the reference's exact call sequence for the prefix and the expert; the
-default applies GeGLU in the gate|up projections' epilogues (and the expert's
-tile layouts, ``Pi05Expert``). Weights are random with the published shapes
+selects the reference's exact call sequence (raw accumulators rescaled by
+``dequant_rows``, GELU / GeGLU requantization of raw accumulators); the default
+writes the rescaled q|k|v (fp16) and projector rows (float32) from the GEMM
+epilogue, applies GELU / GeGLU in the fc1 / gate|up epilogues, and runs the
+expert in its tile layouts (``Pi05Expert``). Weights are random with the published shapes
 (no checkpoint here); ``random_pi05_weights`` draws them on the device.
 """
 from __future__ import annotations
@@ -198,10 +200,14 @@ class Pi05Engine:
         note("norm", res=self.vx, weight=L0.ln1_w, beta=L0.ln1_b, q=q8(T, VIS_D), s=s[0])
         view = (V, VISION_TOKENS, VIS_HEADS, VIS_HD)
         for i, L in enumerate(w.vision):
-            gemm(q8(T, VIS_D), L.qkv, raw(T, 3 * VIS_D))
-            note("gemm", a=q8(T, VIS_D), w=L.qkv, out=raw(T, 3 * VIS_D))
-            dequant_rows(raw(T, 3 * VIS_D), self.vqkv, row=s[0], col=L.qkv.scale, bias=L.qkv.bias)
-            note("dequant", x=raw(T, 3 * VIS_D), y=self.vqkv, row=s[0], w=L.qkv)
+            if self.reference_calls:
+                gemm(q8(T, VIS_D), L.qkv, raw(T, 3 * VIS_D))
+                note("gemm", a=q8(T, VIS_D), w=L.qkv, out=raw(T, 3 * VIS_D))
+                dequant_rows(raw(T, 3 * VIS_D), self.vqkv, row=s[0], col=L.qkv.scale, bias=L.qkv.bias)
+                note("dequant", x=raw(T, 3 * VIS_D), y=self.vqkv, row=s[0], w=L.qkv)
+            else:  # rescaled fp16 rows straight from the epilogue
+                linear(q8(T, VIS_D), s[0], L.qkv, out=self.vqkv)
+                note("qkv16", a=q8(T, VIS_D), sa=s[0], w=L.qkv, out=self.vqkv)
             qkv = self.vqkv.view(V, VISION_TOKENS, 3, VIS_HEADS, VIS_HD)
             attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], out=self.vo.view(view), scale=VIS_HD ** -0.5)
             note("attention", q=qkv[:, :, 0], k=qkv[:, :, 1], v=qkv[:, :, 2], out=self.vo.view(view))
@@ -235,10 +241,14 @@ class Pi05Engine:
             note("norm", res=self.vx, delta=raw(T, VIS_D), delta_row=s[1], w=L.fc2,
                  weight=nxt.ln1_w if nxt else w.post_ln_w, beta=nxt.ln1_b if nxt else w.post_ln_b,
                  q=q8(T, VIS_D), s=s[0])
-        gemm(q8(T, VIS_D), w.projector, raw(T, LM_D))
-        note("gemm", a=q8(T, VIS_D), w=w.projector, out=raw(T, LM_D))
-        dequant_rows(raw(T, LM_D), self.px[:T], row=s[0], col=w.projector.scale, bias=w.projector.bias)
-        note("dequant", x=raw(T, LM_D), y=self.px[:T], row=s[0], w=w.projector)
+        if self.reference_calls:
+            gemm(q8(T, VIS_D), w.projector, raw(T, LM_D))
+            note("gemm", a=q8(T, VIS_D), w=w.projector, out=raw(T, LM_D))
+            dequant_rows(raw(T, LM_D), self.px[:T], row=s[0], col=w.projector.scale, bias=w.projector.bias)
+            note("dequant", x=raw(T, LM_D), y=self.px[:T], row=s[0], w=w.projector)
+        else:  # float32 prefix rows straight from the epilogue
+            linear(q8(T, VIS_D), s[0], w.projector, out=self.px[:T])
+            note("projector", a=q8(T, VIS_D), sa=s[0], w=w.projector, out=self.px[:T])
 
     def prefix(self, M):
         """engines/pi05/engine.py:192-216 over M rows (image rows, then the
