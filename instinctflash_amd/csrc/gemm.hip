@@ -570,9 +570,9 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
   };
 
-  if constexpr (FM == 4) {
-    // Register-pipelined 4-wave form (wave tile 128 x 128, accumulators in
-    // AccVGPRs). A 128-byte stage holds two 32x32x64 K steps (halves); the
+  if constexpr (FM == 4 || (FM == 2 && BM == 128)) {
+    // Register-pipelined 4-wave form (wave tile 128 x 128 for 256-token tiles,
+    // 64 x 128 for 128-token tiles; accumulators in AccVGPRs). A 128-byte stage holds two 32x32x64 K steps (halves); the
     // fragments of the next half are read from LDS into the other register
     // set while the MFMAs of the current half run, so the matrix pipe does not
     // wait on LDS latency. Per stage kt:
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     //   is in LDS and slot kt is free);
     //   half 1: MFMAs on (kt, 1), reads of (kt+1, 0), and the DMA of stage
     //   kt+2 into slot kt, one instruction after each MFMA.
-    static_assert(KB == 128 && STAGES == 2 && kFM == 4 && (kFN == 3 || kFN == 4), "4-wave layout");
+    static_assert(KB == 128 && STAGES == 2 && kWaves == 4 && kFN >= 3 && kFN <= 4, "4-wave layout");
     constexpr int kMF = kFN * kFM;        // MFMAs per half
     constexpr int kRd = 2 * (kFN + kFM);  // 16-byte LDS reads per half
     static_assert(kLoads <= kRd && kLoads % 2 == 0, "one DMA per LDS read");
@@ -1423,9 +1423,11 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 //    12.4 -> 10.6 us; at 256 or more the 64-token tiles win: 1024 x 2560 x 2048
 //    12.2 against 15.2 us);
 //  * kNarrow: fewer than 192 tiles and a longer K -- 128 tokens x 256 weight
-//    rows, 8 waves of 128 x 32, 128-byte stages, one workgroup per CU, plus
-//    split K (1024 x 2048 x 11008: 41 us; 44 us with 4 waves of 128 x 64 and
-//    64-byte stages, 67 us for small tiles without a split).
+//    rows, the register-pipelined 4 waves of 64 x 128 when the 32-bit DMA
+//    offsets fit (else 8 waves of 128 x 32), 128-byte stages, plus split K
+//    (816 x 2048 x 16384: 44.1 -> 42.8 us for the pipelined form; 1024 x 2048 x
+//    11008: 38 us; 44 us with 4 waves of 128 x 64 and 64-byte stages, 67 us for
+//    small tiles without a split).
 enum class BigCfg { kWide, kWide192, kSmall, kSmall32, kNarrow };
 
 inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
@@ -1471,6 +1473,8 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
     case BigCfg::kSmall32:
       return launch_big<32, 128, 128, 2, 4, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     default:
+      if (dma32_ok(e.M, e.N, lda, ldw))
+        return launch_big<128, 256, 128, 2, 1, GLU, 2>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       return launch_big<128, 256, 128, 2, 1, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
 }
