@@ -494,7 +494,8 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
   constexpr int kEpiBytes = kWaves * 32 * kPitch * 4;
   constexpr int kSmem = STAGES * kStage > kEpiBytes ? STAGES * kStage : kEpiBytes;
-  static_assert(OCC * kSmem <= 160 * 1024, "LDS");
+  // the token scales (s_sa) share the CU's LDS with the stage ring
+  static_assert(OCC * (kSmem + BM * 4) <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   __shared__ float s_sa[BM];
 
@@ -1414,14 +1415,18 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 //    K = 14336; a GLU output of 1024 x 22016 is 344 tiles of 256 but 460 of 192.
 //  * kSmall: fewer than 192 tiles of 256 x 256 and K <= 4096 -- 64 tokens x
 //    128 weight rows, 128-byte stages, 4 waves of 64 x 32 (short MFMA chains
-//    per wave: the loop is latency-bound at these sizes), two workgroups per
-//    CU, usually no split (1024 x 2560 x 2048: 28 us with split-K narrow tiles,
-//    15.7 us with 2 waves of 64 x 64 and 64-byte stages, 12.1 us now);
-//  * kSmall32: as kSmall with 32-token tiles (2 waves of 64 x 32, four
-//    workgroups per CU) when 64-token tiles would give fewer than 256
-//    workgroups (200 x 2560 x 2048 10.7 -> 8.8 us, 512 x 1024 x 2048
-//    12.4 -> 10.6 us; at 256 or more the 64-token tiles win: 1024 x 2560 x 2048
-//    12.2 against 15.2 us);
+//    per wave: the loop is latency-bound at these sizes), a 3-stage ring, two
+//    workgroups per CU, usually no split (1024 x 2560 x 2048: 28 us with split-K
+//    narrow tiles, 15.7 us with 2 waves of 64 x 64 and 64-byte stages, 12.1 us
+//    with a 2-stage ring; weights streamed from HBM with bias and residual,
+//    2 -> 3 stages: 1024 x 2560 18.2 -> 15.5 us, 1024 x 2048 15.5 -> 12.3 us);
+//  * kSmall32: as kSmall with 32-token tiles (2 waves of 64 x 32) when 64-token
+//    tiles would give fewer than 256 workgroups (200 x 2560 x 2048 10.7 -> 8.8 us,
+//    512 x 1024 x 2048 12.4 -> 10.6 us; at 256 or more the 64-token tiles win:
+//    1024 x 2560 x 2048 12.2 against 15.2 us). A 4-stage ring when the grid fits
+//    one workgroup per CU, else 3 stages and two per CU (streamed weights: 200 x
+//    2560 x 2048 16.2 -> 10.5 us, 300 x 3072 x 3072 23.0 -> 14.4 us, 816 x 2048 x
+//    2048 16.7 -> 14.0 us against 2 stages);
 //  * kNarrow: fewer than 192 tiles and a longer K -- 128 tokens x 256 weight
 //    rows, the register-pipelined 4 waves of 64 x 128 when the 32-bit DMA
 //    offsets fit (else 8 waves of 128 x 32), 128-byte stages, plus split K
@@ -1469,9 +1474,15 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
         return launch_big<256, 256, 128, 2, 1, GLU, 4>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       return launch_big<256, 256, 128, 2, 1, GLU>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
     case BigCfg::kSmall:
-      return launch_big<64, 128, 128, 2, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
-    case BigCfg::kSmall32:
-      return launch_big<32, 128, 128, 2, 4, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      return launch_big<64, 128, 128, 3, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+    case BigCfg::kSmall32: {
+      // a grid that fits one workgroup per CU takes a 4-stage ring (80 KB);
+      // larger grids 3 stages, two workgroups per CU
+      const BigPlan p = big_plan(e.M, e.N, K, 32, 128, 128);
+      if (p.tiles_m * p.tiles_n * p.ksplit <= 256)
+        return launch_big<32, 128, 128, 4, 1, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+      return launch_big<32, 128, 128, 3, 2, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+    }
     default:
       if (dma32_ok(e.M, e.N, lda, ldw))
         return launch_big<128, 256, 128, 2, 1, GLU, 2>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
