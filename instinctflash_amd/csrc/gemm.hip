@@ -578,12 +578,14 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     // set while the MFMAs of the current half run, so the matrix pipe does not
     // wait on LDS latency. Per stage kt:
     //   half 0: MFMAs on (kt, 0), reads of (kt, 1);
-    //   s_waitcnt lgkmcnt(0) (this wave is done reading slot kt) and vmcnt(0)
-    //   (its DMA of stage kt+1 landed); s_barrier (for every wave: stage kt+1
-    //   is in LDS and slot kt is free);
+    //   s_waitcnt lgkmcnt(0) (this wave is done reading slot kt) and vmcnt
+    //   (its DMA of stage kt+1 landed; those of the STAGES-2 later stages may
+    //   stay in flight); s_barrier (for every wave: stage kt+1 is in LDS and
+    //   slot kt is free);
     //   half 1: MFMAs on (kt, 1), reads of (kt+1, 0), and the DMA of stage
-    //   kt+2 into slot kt, one instruction after each MFMA.
-    static_assert(KB == 128 && STAGES == 2 && kWaves == 4 && kFN >= 3 && kFN <= 4, "4-wave layout");
+    //   kt+STAGES into slot kt, one instruction after each MFMA.
+    static_assert(KB == 128 && (STAGES == 2 || STAGES == 3) && kWaves == 4 && kFN >= 3 && kFN <= 4,
+                  "4-wave layout");
     constexpr int kMF = kFN * kFM;        // MFMAs per half
     constexpr int kRd = 2 * (kFN + kFM);  // 16-byte LDS reads per half
     static_assert(kLoads <= kRd && kLoads % 2 == 0, "one DMA per LDS read");
@@ -635,21 +637,22 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     };
-    // prologue: stages 0 and 1 in flight, stage 0 landed, its half-0 fragments read
+    // prologue: stages 0 .. STAGES-1 in flight, stage 0 landed, its half-0 fragments read
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) dma_one(0, i);
-    if (nk > 1) {
 #pragma unroll
-      for (int i = 0; i < kLoads; ++i) dma_one(1, i);
-      wait_vmcnt<kLoads>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    for (int s = 1; s < STAGES; ++s)
+      if (s < nk) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) dma_one(s, i);
+      }
+    if (nk >= STAGES) wait_vmcnt<(STAGES - 1) * kLoads>();
+    else wait_vmcnt<0>();
     sync();
 #pragma unroll
     for (int r = 0; r < kRd; ++r) read_one(smem, fr[0], 0, r);
     auto stage = [&](int kt, auto dma_tag) {
-      constexpr bool kDma = decltype(dma_tag)::value;  // stage kt + 2 exists
+      constexpr bool kDma = decltype(dma_tag)::value;  // stage kt + STAGES exists
       const uint8_t* cur = smem + (kt % STAGES) * kStage;
       const uint8_t* nxt = smem + ((kt + 1) % STAGES) * kStage;  // after the last stage: a settled slot, unused
       wait_lgkm0();
@@ -660,20 +663,21 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       }
       interleave();
       wait_lgkm0();
-      if (kDma || kt + 1 < nk) wait_vmcnt<0>();
+      if (kDma || kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();  // stages up to kt+STAGES-1 issued
+      else if (kt + 1 < nk) wait_vmcnt<0>();
       sync();
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
         if (m < kMF) mfma_one(fr[1], m);
         read_one(nxt, fr[0], 0, m);
         if constexpr (kDma) {
-          if (m < kLoads) dma_one(kt + 2, m);
+          if (m < kLoads) dma_one(kt + STAGES, m);
         }
       }
       interleave();
     };
     int kt = 0;
-    for (; kt + 2 < nk; ++kt) stage(kt, std::true_type{});
+    for (; kt + STAGES < nk; ++kt) stage(kt, std::true_type{});
     for (; kt < nk; ++kt) stage(kt, std::false_type{});
     wait_vmcnt<0>();  // no DMA may still write LDS when the epilogue reuses it
   } else {
@@ -1428,11 +1432,13 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 //    2560 x 2048 16.2 -> 10.5 us, 300 x 3072 x 3072 23.0 -> 14.4 us, 816 x 2048 x
 //    2048 16.7 -> 14.0 us against 2 stages);
 //  * kNarrow: fewer than 192 tiles and a longer K -- 128 tokens x 256 weight
-//    rows, the register-pipelined 4 waves of 64 x 128 when the 32-bit DMA
-//    offsets fit (else 8 waves of 128 x 32), 128-byte stages, plus split K
-//    (816 x 2048 x 16384: 44.1 -> 42.8 us for the pipelined form; 1024 x 2048 x
-//    11008: 38 us; 44 us with 4 waves of 128 x 64 and 64-byte stages, 67 us for
-//    small tiles without a split).
+//    rows, the register-pipelined 4 waves of 64 x 128 with a 3-stage ring
+//    (144 KB) when the 32-bit DMA offsets fit (else 8 waves of 128 x 32, two
+//    stages), 128-byte stages, plus split K. 816 x 2048 x 16384: 44.1 us with 8
+//    waves, 42.8 pipelined with two stages, 41.0 with three; with the weights
+//    streamed from HBM 52.0 -> 42.4 us (two -> three stages), 1024 x 2048 x 11008
+//    44.2 -> 39.3 us. (44 us with 4 waves of 128 x 64 and 64-byte stages, 67 us
+//    for small tiles without a split.)
 enum class BigCfg { kWide, kWide192, kSmall, kSmall32, kNarrow };
 
 inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
@@ -1485,7 +1491,7 @@ int launch_large(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, i
     }
     default:
       if (dma32_ok(e.M, e.N, lda, ldw))
-        return launch_big<128, 256, 128, 2, 1, GLU, 2>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
+        return launch_big<128, 256, 128, 3, 1, GLU, 2>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
       return launch_big<128, 256, 128, 2, 1, GLU, 1>(a, lda, w, ldw, K, e, ws, ws_bytes, st);
   }
 }
