@@ -316,16 +316,31 @@ def test_workspace_reuse_across_shapes(gpu, oracle_mod):
 
 
 @pytest.mark.parametrize("M,N,K,act", [(816, 2048, 16384, None), (512, 1024, 2048, None), (300, 1024, 4096, "swiglu"),
-                                       (1024, 2048, 11008, None), (257, 512, 2048, "gelu_tanh")])
+                                       (1024, 2048, 11008, None), (257, 512, 2048, "gelu_tanh"),
+                                       (128, 4096, 2048, "geglu"), (100, 256, 16384, None), (200, 768, 8192, "gelu_tanh")])
 def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
-    # few output tiles: the large-M kernel splits K and a reduce kernel applies the epilogue
+    # few output tiles: the large-M kernel splits K and a reduce kernel adds the
+    # partials in slice order and applies the epilogue (100 x 256 x 16384: one
+    # tile, 32 slices)
     from instinctflash_amd import _lib
-    from instinctflash_amd.kernels import pack_glu
-    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, 0) > 0
+    from instinctflash_amd.kernels import fp8 as F, pack_glu
+    glu = act in ("geglu", "swiglu")
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) > 1024
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N, bias=True)
-    res = torch.randn((M, N // 2 if act == "swiglu" else N), generator=g).to(torch.bfloat16)
-    w = pack_glu(fw) if act == "swiglu" else fw
-    _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    w = pack_glu(fw) if glu else fw
+    o32, o16 = _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+    # repeated calls: bit-identical (fixed slice order) and the counters return to zero
+    for _ in range(3):
+        again = F.linear(qa, sa, w, act=act, residual=res.to(gpu), out_dtype=torch.float32)
+        assert torch.equal(again.view(torch.int32), o32.view(torch.int32))
+    torch.cuda.synchronize()
+    for ws in F._WORKSPACES.values():
+        assert int(ws[:1024].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
+    # in place: out aliases the residual
+    r = res.to(gpu).clone()
+    F.linear(qa, sa, w, out=r, act=act, residual=r)
+    assert torch.equal(r.view(torch.int16), o16.view(torch.int16))
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])
