@@ -911,10 +911,26 @@ __global__ __launch_bounds__(256) void splitk_reduce(Partials part, int ksplit, 
   const int64_t c = (idx - m * groups) * 4;                 // output column
   const int64_t ng = GLU ? (c >> 4) * 32 + (c & 15) : c;   // packed row of its (gate) group
   v4f a = v4f{0.f, 0.f, 0.f, 0.f}, u = a;
-  for (int s = 0; s < ksplit; ++s) {
-    const float* row = part.base + (s * e.M + m) * part.ld;
-    a += *reinterpret_cast<const v4f*>(row + ng);
-    if constexpr (GLU) u += *reinterpret_cast<const v4f*>(row + ng + 16);
+  const float* p0 = part.base + m * part.ld + ng;
+  const int64_t slice = e.M * part.ld;
+  int s = 0;
+  // four slices' loads in flight at a time, added in slice order
+  for (; s + 4 <= ksplit; s += 4) {
+    v4f pa[4], pu[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pa[q] = *reinterpret_cast<const v4f*>(p0 + (s + q) * slice);
+      if constexpr (GLU) pu[q] = *reinterpret_cast<const v4f*>(p0 + (s + q) * slice + 16);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a += pa[q];
+      if constexpr (GLU) u += pu[q];
+    }
+  }
+  for (; s < ksplit; ++s) {
+    a += *reinterpret_cast<const v4f*>(p0 + s * slice);
+    if constexpr (GLU) u += *reinterpret_cast<const v4f*>(p0 + s * slice + 16);
   }
   float y[4];
   if constexpr (GLU) epi_pre_glu(e, a, u, ng, m, y);
