@@ -343,6 +343,24 @@ def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
     assert torch.equal(r.view(torch.int16), o16.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,N,K,act", [
+    (100, 256, 128, None), (100, 256, 256, "gelu_tanh"), (100, 256, 384, None),  # 32-token tiles, 4-stage ring
+    (600, 2048, 256, None), (1024, 2048, 256, None),  # 3-stage rings with fewer K stages than slots
+    (1024, 2048, 384, "swiglu"),
+    (300, 512, 4736, None),  # 128 x 256 split tiles: 8 slices of 5 stages, the last of 2
+    (300, 512, 5248, "gelu_tanh"),  # 9 slices of 5 stages, the last of 1
+])
+def test_ring_depth_edges(gpu, oracle_mod, M, N, K, act):
+    # K shorter than the operand ring, and split-K slices shorter than the ring,
+    # in the 3- and 4-stage rings of the small-grid and split tiles
+    from instinctflash_amd.kernels import pack_glu
+    glu = act in ("geglu", "swiglu")
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M * 7 + K, bias=True)
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    w = pack_glu(fw) if glu else fw
+    _check(gpu, oracle_mod, qa, sa, w, f"ring {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])
 def test_skinny_shorter_k_is_not_split(gpu, M, N, K):
     # K < 64 steps: one workgroup per row group (the split's round trip costs more)
