@@ -361,6 +361,42 @@ def test_ring_depth_edges(gpu, oracle_mod, M, N, K, act):
     _check(gpu, oracle_mod, qa, sa, w, f"ring {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
 
 
+@pytest.mark.parametrize("case", ["wide", "wide_glu", "narrow"])
+def test_operands_past_4gib(gpu, oracle_mod, case):
+    # An activation operand spanning >= 4 GiB (the 4-wave loops form 32-bit DMA
+    # offsets): the 8-wave forms run -- 256 x 256 tiles (GLU: the 256 x 192 choice
+    # falls back to them), and 128 x 256 split-K tiles over a row-strided operand.
+    # Sampled rows against the oracle, rows past the 4 GiB offset included.
+    from instinctflash_amd.kernels import linear, pack_glu, quantize_weight
+    if case == "narrow":  # 126 tiles of 128 x 256: K split in two
+        M, N, K, lda = 16100, 256, 4224, 268448
+    else:
+        M, N, K, lda = 524544, 512 if case == "wide_glu" else 256, 8192, 8192
+    assert M * lda >= 1 << 32 and M < 1 << 24
+    print(f"[4gib] {case} {M}x{N}x{K} lda={lda}", flush=True)
+    gg = torch.Generator(device=gpu).manual_seed(11)
+    buf = torch.randint(0, 256, (M, lda), dtype=torch.uint8, device=gpu, generator=gg)
+    buf.bitwise_and_(0xBF)  # exponent field <= 7: |x| <= 1.875, no NaN codes
+    a = buf[:, :K].view(torch.float8_e4m3fn)
+    sa = torch.rand(M, device=gpu, generator=gg) + 0.5
+    g = torch.Generator().manual_seed(12)
+    fw = quantize_weight(torch.randn((N, K), generator=g) * 0.02, torch.randn(N, generator=g) * 0.01, device=gpu)
+    act = "swiglu" if case == "wide_glu" else None
+    w = pack_glu(fw) if act else fw
+    out = linear(a, sa, w, act=act, out_dtype=torch.float32)
+    ob = linear(a, sa, w, act=act, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    first_past = (1 << 32) // lda + 1  # first row whose bytes start past 4 GiB
+    rows = np.unique(np.concatenate([np.array([0, 1, M // 2, first_past - 1, first_past, M - 2, M - 1]),
+                                     np.random.default_rng(3).choice(M, 57, replace=False)]))
+    ridx = torch.as_tensor(rows, device=gpu)
+    ref = oracle_mod.ref_linear(_q(a[ridx]), _f(sa[ridx]), _q(fw.w), _f(fw.scale), bias=_f(fw.bias), act=act)
+    _assert_close(_f(out[ridx]), ref, f"4gib {case}")
+    assert torch.equal(ob[ridx].view(torch.int16), out[ridx].to(torch.bfloat16).view(torch.int16))
+    del buf, a, out, ob
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])
 def test_skinny_shorter_k_is_not_split(gpu, M, N, K):
     # K < 64 steps: one workgroup per row group (the split's round trip costs more)
