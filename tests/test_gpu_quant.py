@@ -110,6 +110,25 @@ def test_strided_rows(gpu, oracle_mod):
     assert not _q(qbig[:, :512]).any() and not _q(qbig[:, 1536:]).any()
 
 
+def test_rows_past_4gib(gpu, oracle_mod):
+    # bf16 input of 4.3 GB and its 2.1 GB e4m3 output: 64-bit row addressing;
+    # sampled rows (those past the 4 GiB input offset included) bit-exact
+    from instinctflash_amd.kernels import quant_rows
+    M, K = 262400, 8192
+    assert M * K * 2 >= 1 << 32
+    gg = torch.Generator(device=gpu).manual_seed(21)
+    x = torch.randn((M, K), device=gpu, generator=gg, dtype=torch.bfloat16)
+    q, s = quant_rows(x)
+    torch.cuda.synchronize()
+    first_past = (1 << 32) // (2 * K)
+    rows = torch.as_tensor([0, M // 2, first_past - 1, first_past, first_past + 77, M - 1], device=gpu)
+    eq, es = oracle_mod.quant_rows(_bits(x[rows]))
+    assert np.array_equal(_f(s[rows]).view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(_q(q[rows]), eq)
+    del x, q, s
+    torch.cuda.empty_cache()
+
+
 def test_empty_rows(gpu):
     from instinctflash_amd.kernels import quant_rows
     q, s = quant_rows(torch.empty((0, 64), dtype=torch.bfloat16, device=gpu))
