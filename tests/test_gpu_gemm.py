@@ -193,7 +193,8 @@ def test_ragged_small_grid_configs(gpu, oracle_mod, K, act, resgate):
 
 
 @pytest.mark.parametrize("M,N,K,act", [(65, 256, 1040, None), (100, 768, 528, "gelu_tanh"), (300, 512, 1552, "geglu"),
-                                       (1000, 2112, 1040, None), (2048, 8192, 272, "swiglu")])
+                                       (1000, 2112, 1040, None), (2048, 8192, 272, "swiglu"),
+                                       (2048, 4096, 272, None)])
 def test_unaligned_k_lds_path(gpu, oracle_mod, M, N, K, act):
     # M > 64 with K % 128 != 0 runs the register-staged LDS kernel (everything
     # else past the skinny range runs the large-M kernel): 64x64 tiles under one
@@ -361,15 +362,17 @@ def test_ring_depth_edges(gpu, oracle_mod, M, N, K, act):
     _check(gpu, oracle_mod, qa, sa, w, f"ring {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
 
 
-@pytest.mark.parametrize("case", ["wide", "wide_glu", "narrow"])
+@pytest.mark.parametrize("case", ["wide", "wide_glu", "wide192", "narrow", "narrow_glu"])
 def test_operands_past_4gib(gpu, oracle_mod, case):
     # An activation operand spanning >= 4 GiB (the 4-wave loops form 32-bit DMA
     # offsets): the 8-wave forms run -- 256 x 256 tiles (GLU: the 256 x 192 choice
     # falls back to them), and 128 x 256 split-K tiles over a row-strided operand.
     # Sampled rows against the oracle, rows past the 4 GiB offset included.
     from instinctflash_amd.kernels import linear, pack_glu, quantize_weight
-    if case == "narrow":  # 126 tiles of 128 x 256: K split in two
-        M, N, K, lda = 16100, 256, 4224, 268448
+    if case in ("narrow", "narrow_glu"):  # 126 tiles of 128 x 256: K split in two (plain)
+        M, N, K, lda = 16100, 512 if case == "narrow_glu" else 256, 4224, 268448
+    elif case == "wide192":  # 8192 x 3072: 256 x 192 tiles (two full rounds), row-strided operand
+        M, N, K, lda = 8192, 3072, 3072, 524400
     else:
         M, N, K, lda = 524544, 512 if case == "wide_glu" else 256, 8192, 8192
     assert M * lda >= 1 << 32 and M < 1 << 24
@@ -381,7 +384,7 @@ def test_operands_past_4gib(gpu, oracle_mod, case):
     sa = torch.rand(M, device=gpu, generator=gg) + 0.5
     g = torch.Generator().manual_seed(12)
     fw = quantize_weight(torch.randn((N, K), generator=g) * 0.02, torch.randn(N, generator=g) * 0.01, device=gpu)
-    act = "swiglu" if case == "wide_glu" else None
+    act = "swiglu" if case.endswith("glu") else None
     w = pack_glu(fw) if act else fw
     out = linear(a, sa, w, act=act, out_dtype=torch.float32)
     ob = linear(a, sa, w, act=act, out_dtype=torch.bfloat16)
@@ -395,6 +398,25 @@ def test_operands_past_4gib(gpu, oracle_mod, case):
     assert torch.equal(ob[ridx].view(torch.int16), out[ridx].to(torch.bfloat16).view(torch.int16))
     del buf, a, out, ob
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("M,N,K,act", [
+    (32, 4096, 1024, None), (32, 4096, 4096, None), (40, 4096, 4096, "gelu_tanh"), (64, 4096, 4096, None),
+    (32, 4096, 4096, "swiglu"), (40, 2048, 1024, "geglu"), (64, 16384, 1024, "swiglu"), (48, 8192, 1024, None),
+])
+def test_skinny_token_block_forms(gpu, oracle_mod, M, N, K, act):
+    # 2-4 token blocks per workgroup (256 or more row groups, so no split over
+    # the tokens), with 4 or 8 waves, plain and GLU
+    from instinctflash_amd.kernels import pack_glu
+    glu = act in ("geglu", "swiglu")
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
+    res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
+    w = pack_glu(fw) if glu else fw
+    o32, _ = _check(gpu, oracle_mod, qa, sa, w, f"skinny blocks {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+    # the tile-layout weights: bit-identical
+    from instinctflash_amd.kernels import fp8 as F, pack_skinny
+    got = F.linear(qa, sa, pack_skinny(w), act=act, residual=res.to(gpu), out_dtype=torch.float32)
+    assert torch.equal(got.view(torch.int32), o32.view(torch.int32)), f"tiled skinny blocks {M}x{N}x{K}"
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])

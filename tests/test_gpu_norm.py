@@ -18,11 +18,11 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(M, D, seed, res_dtype=torch.float32, n_tables=0):
+def _inputs(M, D, seed, res_dtype=torch.float32, n_tables=0, delta_dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     t = dict(
         res=torch.randn(M, D, generator=g).to(res_dtype),
-        delta=(torch.randn(M, D, generator=g) * 4).to(torch.bfloat16),
+        delta=(torch.randn(M, D, generator=g) * 4).to(delta_dtype),
         delta_row=torch.rand(M, generator=g), delta_col=torch.rand(D, generator=g),
         bias=torch.randn(D, generator=g), weight=torch.rand(D, generator=g) + 0.5, beta=torch.randn(D, generator=g),
     )
@@ -92,6 +92,16 @@ def test_reference_case(gpu, oracle_mod, layernorm):
 @pytest.mark.parametrize("layernorm", [False, True])
 def test_shapes(gpu, oracle_mod, M, D, layernorm):
     _check(gpu, oracle_mod, _inputs(M, D, M + D), ALL, layernorm, f"{M}x{D} ln={layernorm}")
+
+
+@pytest.mark.parametrize("D", [1024, 3072, 6144, 12288])  # 1, 2, 4, 8 groups of 8 values per lane
+@pytest.mark.parametrize("M", [5, 1030])  # one row per workgroup / the many-rows form (M >= 1024)
+@pytest.mark.parametrize("res_dtype,delta_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                                   (torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32)])
+def test_width_and_dtype_forms(gpu, oracle_mod, D, M, res_dtype, delta_dtype):
+    # every compiled form of the producer: lane width x residual dtype x delta dtype x row form
+    t = _inputs(M, D, M + D, res_dtype=res_dtype, delta_dtype=delta_dtype)
+    _check(gpu, oracle_mod, t, ALL, D % 2048 == 0, f"{M}x{D} res {res_dtype} delta {delta_dtype}")
 
 
 @pytest.mark.parametrize("use", [[], ["weight"], ["mod_scale", "mod_shift"], ["delta"], ["delta", "delta_col"],
