@@ -374,3 +374,66 @@ def test_random_wide_range_stress(gpu, oracle_mod, seed):
         x[:, 64 + k * n:64 + (k + 1) * n] = np.minimum(v, amax[:, None])
     _check_rows(torch.from_numpy(x).to(gpu), oracle_mod)
     _check_rows(torch.from_numpy(x).to(torch.bfloat16).to(gpu), oracle_mod)
+
+
+# Every width form of the row engine (lanes per row x 8-value groups per lane),
+# for each row source: (M, K) pairs that select them -- fewer than 256 rows give
+# each row a whole block (256 / 512 / 1024 lanes), more rows pack 64-256 lanes per
+# row, K % 8 != 0 takes the generic kernel.
+_FORMS = [(20, 1024), (20, 4096), (20, 8192), (20, 16384), (20, 32768), (20, 1004),
+          (260, 512), (260, 1024), (260, 2048), (260, 4096), (260, 8192), (260, 16384), (260, 32768)]
+_SOURCES = ["bf16", "f32", "affine", "affine_col", "affine_bias_gelu", "gelu", "gated_gelu_col", "gated_silu"]
+
+
+@pytest.mark.parametrize("M,K", _FORMS)
+@pytest.mark.parametrize("src", _SOURCES)
+def test_row_engine_forms(gpu, oracle_mod, src, M, K):
+    from instinctflash_amd.kernels import gated_act_quant, quant_rows, row_quant
+    gated = src.startswith("gated")
+    if gated and K > 16384:
+        pytest.skip("gated_act_quant takes hidden widths up to 16384 (the reference's contract)")
+    g = torch.Generator().manual_seed(M * 131 + K + len(src))
+    cols = 2 * K if gated else K
+    x = (torch.randn((M, cols), generator=g) * 2).to(torch.float32 if src == "f32" else torch.bfloat16)
+    row, col = torch.rand(M, generator=g) + 0.5, torch.rand(cols, generator=g) + 0.5
+    bias = torch.randn(cols, generator=g)
+    xf = x.numpy() if src == "f32" else oracle_mod.bf16_to_f32(_bits(x))
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty(M, device=gpu)
+    exact = True
+    if src in ("bf16", "f32"):
+        q, s = quant_rows(x.to(gpu))
+        v = xf
+    elif src.startswith("affine") or src == "gelu":
+        use_col = src in ("affine", "affine_col")
+        use_bias = src in ("affine", "affine_bias_gelu")
+        gelu = src.endswith("gelu")
+        row_quant(x.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu) if use_col else None,
+                  bias=bias.to(gpu) if use_bias else None, gelu=gelu)
+        v = (xf * row.numpy()[:, None]).astype(np.float32)
+        if use_col:
+            v = (v * col.numpy()[None, :]).astype(np.float32)
+        if use_bias:
+            v = (v + bias.numpy()[None, :]).astype(np.float32)
+        if gelu:
+            v, exact = oracle_mod.gelu_tanh(v), False
+    else:
+        use_col = src.endswith("col")
+        act = 0 if "gelu" in src else 1
+        gated_act_quant(x.to(gpu), q, s, row=row.to(gpu), col=col.to(gpu) if use_col else None, act=act)
+        h = (xf * row.numpy()[:, None]).astype(np.float32)
+        if use_col:
+            h = (h * col.numpy()[None, :]).astype(np.float32)
+        gg, uu = h[:, :K], h[:, K:]
+        v, exact = ((oracle_mod.gelu_tanh(gg) if act == 0 else oracle_mod.silu(gg)) * uu).astype(np.float32), False
+    torch.cuda.synchronize()
+    eq, es = oracle_mod.quant_rows(np.ascontiguousarray(v, dtype=np.float32))
+    if exact:
+        assert np.array_equal(_f(s).view(np.uint32), es.view(np.uint32)), f"{src} {M}x{K}: scales"
+        assert np.array_equal(_q(q), eq), f"{src} {M}x{K}: bytes"
+    else:
+        # hardware exp2 / rcp: the bars of the GELU and gated tests above
+        assert np.all(np.abs(_f(s).view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
+        assert (_q(q) == eq).mean() > 0.999
+        err = np.abs(_deq(q, s).cpu().numpy() - v) / np.abs(v).max(axis=1, keepdims=True)
+        assert err.max() < 0.07
