@@ -103,6 +103,20 @@ def test_shapes_bf16(gpu, oracle_mod, B, Tq, Tk, hq, hkv, hd, splits):
     _close(out, _ref(oracle_mod, q, k, v, np.full(Tq, Tk)), torch.bfloat16, f"B{B} Tq{Tq} Tk{Tk} hd{hd}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd,hq,hkv,Tq,splits", [(160, 4, 2, 40, 2), (192, 4, 1, 33, 1), (192, 8, 2, 20, 3),
+                                                 (224, 2, 2, 17, 2), (256, 16, 2, 9, 2)])
+def test_head_dim_forms(gpu, oracle_mod, dtype, hd, hq, hkv, Tq, splits):
+    # head dims 160-224 (5-7 32-dim slices per lane group) in both operand types,
+    # and the split combine at its widest (16 heads x 256 dims over few tokens)
+    from instinctflash_amd.kernels import SplitWorkspace, attention
+    Tk = 150
+    q, k, v = _qkv(1, Tq, Tk, hq, hkv, hd, hd + hq + Tq, dtype)
+    ws = SplitWorkspace(1, Tq, hq, hkv, hd, splits, gpu) if splits > 1 else None
+    out = attention(q.to(gpu), k.to(gpu), v.to(gpu), split=ws)
+    _close(out, _ref(oracle_mod, q, k, v, np.full(Tq, Tk)), dtype, f"hd{hd} hq{hq} {dtype}")
+
+
 def test_engine_views_and_pooled_index(gpu, oracle_mod):
     # q/k/v as strided views of one fused buffer (engines/pi05/engine.py:174), a
     # custom scale, and a pooled cache read through kv_index (wan_va/engine.py:218)

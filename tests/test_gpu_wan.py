@@ -70,7 +70,7 @@ def test_wan5b_shape(gpu, oracle_mod, out_dtype):
     _run_check(gpu, oracle_mod, 2, 64, 24, 128, True, True, out_dtype, 1)
 
 
-@pytest.mark.parametrize("H,HD", [(4, 64), (8, 256), (2, 8), (40, 128)])
+@pytest.mark.parametrize("H,HD", [(4, 64), (8, 256), (2, 8), (40, 128), (48, 256)])
 def test_shapes(gpu, oracle_mod, H, HD):
     _run_check(gpu, oracle_mod, 1, 33, H, HD, True, True, torch.bfloat16, H + HD)
 
