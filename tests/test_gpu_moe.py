@@ -87,7 +87,9 @@ def test_router_strided_rows(gpu, oracle_mod):
 @pytest.mark.parametrize("res_dtype,y_dtype,E,D", [(torch.float32, torch.float32, 32, 768),
                                                    (torch.bfloat16, torch.bfloat16, 32, 768),
                                                    (torch.float32, None, 32, 768), (torch.float32, None, 48, 768),
-                                                   (torch.bfloat16, torch.float32, 16, 2048)])
+                                                   (torch.bfloat16, torch.float32, 16, 2048),
+                                                   (torch.float32, None, 16, 4096), (torch.bfloat16, torch.float32, 16, 8192),
+                                                   (torch.float32, torch.bfloat16, 8, 12288)])
 def test_fused_router_matches_standalone(gpu, res_dtype, y_dtype, E, D):
     # tests/test_gi_kernels.py:206-216, plus bf16 residual / y, no y at all, and
     # shapes outside the prefetched-weights path (E > 32, D > 1024): the fused
@@ -134,9 +136,11 @@ def _check_act(gpu, oracle_mod, gu, row, col, rw, E, G, NR):
     M, F = gu.shape[0], gu.shape[1] // 2
     q = torch.empty(M, F, device=gpu, dtype=torch.float8_e4m3fn)
     qs = torch.empty(M, device=gpu)
-    moe_act_quant(gu.to(gpu), q, qs, rw.to(gpu), row=row.to(gpu), col=col.to(gpu), experts=E, group=G, n_routed=NR)
+    moe_act_quant(gu.to(gpu), q, qs, rw.to(gpu), row=row.to(gpu), col=None if col is None else col.to(gpu),
+                  experts=E, group=G, n_routed=NR)
     torch.cuda.synchronize()
-    h = oracle_mod.moe_act(gu.float().numpy(), row.numpy(), col.numpy(), rw.numpy(), E, G, NR)
+    cn = np.ones(2 * F, np.float32) if col is None else col.numpy()  # no column scale: x 1.0 is exact
+    h = oracle_mod.moe_act(gu.float().numpy(), row.numpy(), cn, rw.numpy(), E, G, NR)
     eq, es = oracle_mod.quant_rows(h)
     got_s = qs.cpu().numpy()
     assert np.all(np.abs(got_s.view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
@@ -163,6 +167,12 @@ def test_act_shapes(gpu, oracle_mod, M, E, G, S, nr):
     gu, row, col, rw = _act_case(M, E, G, S, M + E)
     F = E * G + S
     _check_act(gpu, oracle_mod, gu, row, col, rw, E, G, F if nr == "all" else E * G)
+
+
+@pytest.mark.parametrize("M,E,G,S", [(4, 8, 512, 512), (300, 8, 128, 64), (40, 32, 512, 704)])
+def test_act_without_column_scale(gpu, oracle_mod, M, E, G, S):
+    gu, row, _, rw = _act_case(M, E, G, S, M + G)
+    _check_act(gpu, oracle_mod, gu, row, None, rw, E, G, E * G)
 
 
 def test_contract_errors(gpu):
