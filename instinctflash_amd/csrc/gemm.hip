@@ -782,6 +782,24 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     const bool act_silu = kRt ? (fl & IFX_EPI_SWIGLU) != 0 : (MD & 2) != 0;
     const bool has_gate = kRt ? (fl & IFX_EPI_GATE) != 0 : (MD & 4) != 0;
     const bool has_res = kRt ? (fl & IFX_EPI_RESIDUAL) != 0 : (MD & 8) != 0;
+    // Compile-time residual modes load every residual row of the wave tile
+    // (bf16 x 4 per row and lane) before the first output store and wait for
+    // them once. Vector-memory loads and stores share one completion counter,
+    // so a residual load consumed after a store would wait for that store.
+    // (4-wave 128 x 128 wave tiles only: their accumulators sit in AccVGPRs,
+    // leaving the VGPRs of the K loop's fragments free for the residuals.)
+    constexpr bool kPre = !kRt && (MD & 8) != 0 && kFM == 4;
+    uint2 resv[kPre ? kFM : 1][kPre ? kRowIters : 1];
+    if constexpr (kPre) {
+      const uint16_t* rp = static_cast<const uint16_t*>(e.res) + (col_ok ? c_out : 0);
+#pragma unroll
+      for (int j = 0; j < kFM; ++j)
+#pragma unroll
+        for (int t = 0; t < kRowIters; ++t) {
+          const int64_t m = min(mw + j * 32 + r0 + t * kRowsPerPass, e.M - 1);
+          resv[j][t] = *reinterpret_cast<const uint2*>(rp + m * e.ldr);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < kFM; ++j) {
 #pragma unroll
@@ -790,10 +808,19 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
         for (int q = 0; q < 4; ++q)
           *reinterpret_cast<v4f*>(tile + frow * kPitch + i * 32 + 8 * q + 4 * fhalf) = quad(acc[i][j], q);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if constexpr (kPre) {
+        if (j == 0) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every residual row has landed
+      }
       const int64_t mrow = mw + j * 32 + r0;         // token of pass 0
       const int64_t left = e.M - (mw + j * 32);      // rows of this fragment row inside M
-      // residual rows are loaded kResBatch at a time, ahead of their math
-      constexpr int kResBatch = kRowIters < 8 ? kRowIters : 8;
+      // Rows that load their residuals here do so kResBatch rows at a time,
+      // ahead of their math. The other modes walk all rows as one batch, with
+      // no loop: the compiler waits for every outstanding
+      // vector-memory operation (the previous fragment row's stores included)
+      // at the entry of a loop that stores, which left each fragment row's
+      // store latency exposed (8192x14336x3072 GELU 312 -> 302 us).
+      constexpr bool kRowLoads = kRt || ((MD & 8) != 0 && !kPre);
+      constexpr int kResBatch = !kRowLoads ? kRowIters : kRowIters < 8 ? kRowIters : 8;
       // A fragment row wholly inside M runs without per-row guards, so the
       // compiler can interleave the rows' arithmetic.
       auto emit = [&](auto full_tag) __attribute__((always_inline)) {
@@ -812,9 +839,13 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
             res[tb] = (has_res && (kFull || r < left)) ? load_res4(e, mrow + t * kRowsPerPass, c_out)
                                             : make_float4(0.f, 0.f, 0.f, 0.f);
           } else if constexpr ((MD & 8) != 0) {
-            const uint16_t* rp = static_cast<const uint16_t*>(e.res) + c_out;
-            const int64_t m = min(mrow + t * kRowsPerPass, e.M - 1);
-            const uint2 rv = *reinterpret_cast<const uint2*>(rp + m * e.ldr);
+            uint2 rv;
+            if constexpr (kPre) {
+              rv = resv[j][t];
+            } else {
+              const uint16_t* rp = static_cast<const uint16_t*>(e.res) + c_out;
+              rv = *reinterpret_cast<const uint2*>(rp + min(mrow + t * kRowsPerPass, e.M - 1) * e.ldr);
+            }
             res[tb] = make_float4(__uint_as_float(rv.x << 16), __uint_as_float(rv.x & 0xFFFF0000u),
                                  __uint_as_float(rv.y << 16), __uint_as_float(rv.y & 0xFFFF0000u));
           }
