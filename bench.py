@@ -121,6 +121,60 @@ def measure_calls(wl, launches):
     return out
 
 
+def measure_vendor(wl, calls, launches):
+    """The vendor library on the same GEMM shapes: hipBLASLt FP8 through
+    torch._scaled_mm (e4m3 x e4m3, per-token and per-channel fp32 scales,
+    bf16 out, the reference's GEMM call: instinctflash/kernels/fp8.py:50-53),
+    µs per call in a graph of back-to-back calls (median of 5), weights rotating
+    through a pool of the workload's size as in the step. hipBLASLt fuses only
+    the scales: no bias, activation, gate or residual, and a GLU projection
+    writes both halves (2F columns), so its bytes are a lower bound of the
+    reference path's. Returns None if this torch build lacks row-wise scaling."""
+    import torch
+    from instinctflash_amd.kernels import fp8 as F
+    gemms = [c for c in wl.calls() if c.kind == "gemm"]
+    ours = {c["call"]: c["us_p50"] for c in calls if c["kind"] == "gemm"}
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(7)
+    side = torch.cuda.Stream()
+    rows, ours_sum, vendor_sum = [], 0.0, 0.0
+    for c in gemms:
+        w = c.work
+        a, sa = F.quant_rows(torch.randn((w.M, w.K), generator=g).to(torch.bfloat16).to(dev))
+        pool = max(1, wl.pool)
+        ws = [F.quantize_weight(torch.randn((w.N, w.K), generator=g) * 0.02, device=dev)] if pool == 1 else None
+        if ws is None:
+            base = F.quantize_weight(torch.randn((w.N, w.K), generator=g) * 0.02, device=dev)
+            ws = [base] + [F.Fp8Weight(base.w.clone(), base.scale.clone()) for _ in range(pool - 1)]
+        out = torch.empty((w.M, w.N), dtype=torch.bfloat16, device=dev)
+        sa2 = sa.view(-1, 1)
+        sws = [x.scale.view(1, -1) for x in ws]
+
+        def fn(i, ws=ws, sws=sws, a=a, sa2=sa2, out=out):
+            k = i % len(ws)
+            torch._scaled_mm(a, ws[k].w.t(), scale_a=sa2, scale_b=sws[k], out_dtype=torch.bfloat16, out=out)
+        try:
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                fn(0)
+            torch.cuda.synchronize()
+        except (RuntimeError, NotImplementedError) as exc:  # no row-wise FP8 in this build
+            _log(f"[bench] hipBLASLt comparator unavailable: {exc}")
+            return None
+        gr = capture(fn, launches, side)
+        time_graph(gr)
+        us = sorted(time_graph(gr)[0] / launches * 1e3 for _ in range(5))[2]
+        del gr, ws
+        rows.append({"call": c.name, "shape": f"{w.M}x{w.N}x{w.K}", "us_p50": round(us, 3),
+                     "tflops": round(w.flops / us / 1e6, 2), "ours_us_p50": ours.get(c.name)})
+        vendor_sum += us
+        ours_sum += ours.get(c.name, 0.0)
+    torch.cuda.empty_cache()
+    return {"library": "hipBLASLt via torch._scaled_mm (row-wise scales, bf16 out, no fused epilogue)",
+            "calls": rows, "gemm_us_sum": round(vendor_sum, 2), "ours_gemm_us_sum": round(ours_sum, 2),
+            "speedup_ours_vs_vendor": round(vendor_sum / ours_sum, 3) if ours_sum else None}
+
+
 def summarize(wl, m):
     step_s = m["step_ms"] * 1e-3
     d = wl.dominant_gemm
@@ -598,6 +652,7 @@ def main():
         results[key]["steps"] = steps
         results[key]["roofline"] = roofline(wl, m)
         results[key]["calls"] = measure_calls(wl, 32 if wl.bound == "hbm" else 8)
+        results[key]["hipblaslt"] = measure_vendor(wl, results[key]["calls"], 32 if wl.bound == "hbm" else 8)
         if key == args.config:
             head_m = m
             results[key]["roofline"].update(measure_sclk(wl, m["kernel_ms"]))
