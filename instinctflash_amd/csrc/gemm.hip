@@ -60,7 +60,23 @@ struct Epi {
   int64_t ldo;
   int flags;
   int64_t M, N;
+  int nt_out = 0;        // 1: large-M bf16 output rows stored nontemporally
 };
+
+// 8-byte nontemporal load / store (residual rows are read once; large
+// outputs are written once and read back only after the next kernels'
+// traffic has passed through the caches).
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld8_nt(const void* p) {
+  const v2u t = __builtin_nontemporal_load(static_cast<const v2u*>(p));
+  return make_uint2(t.x, t.y);
+}
+__device__ __forceinline__ void st8_nt(void* p, uint2 v) {
+  v2u t;
+  t.x = v.x;
+  t.y = v.y;
+  __builtin_nontemporal_store(t, static_cast<v2u*>(p));
+}
 
 __device__ __forceinline__ float4 load_f4_or(const float* p, int64_t i, float dflt) {
   if (!p) return make_float4(dflt, dflt, dflt, dflt);
@@ -797,7 +813,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 #pragma unroll
         for (int t = 0; t < kRowIters; ++t) {
           const int64_t m = min(mw + j * 32 + r0 + t * kRowsPerPass, e.M - 1);
-          resv[j][t] = *reinterpret_cast<const uint2*>(rp + m * e.ldr);
+          resv[j][t] = ld8_nt(rp + m * e.ldr);
         }
     }
 #pragma unroll
@@ -892,7 +908,9 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
                 uint2 o;
                 o.x = pack_bf16x2(y[0], y[1]);
                 o.y = pack_bf16x2(y[2], y[3]);
-                *reinterpret_cast<uint2*>(orow + static_cast<int64_t>(t * kRowsPerPass) * e.ldo) = o;
+                uint16_t* op = orow + static_cast<int64_t>(t * kRowsPerPass) * e.ldo;
+                if (e.nt_out) st8_nt(op, o);
+                else *reinterpret_cast<uint2*>(op) = o;
               }
             }
           }
@@ -1601,6 +1619,11 @@ int check_linear(const void* w, int64_t ldw, const float* sw, const float* bias,
   return IFX_OK;
 }
 
+// Large-M outputs of at least this many bytes are stored nontemporally, so
+// that they do not displace the operands that later kernels find in the
+// 256 MB memory-side cache.
+constexpr int64_t kNtOutBytes = int64_t(32) << 20;
+
 inline size_t round256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 // Workspace of ifx_quant_linear: the GEMM's own workspace first (its ticket
@@ -1647,9 +1670,17 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
     return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
                : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   }
-  if (big_path(M, K))
+  if (big_path(M, K)) {
+    const int64_t out_bytes = M * (glu ? N / 2 : N) * static_cast<int64_t>(sizeof(uint16_t));
+#ifdef X_ENV
+    int64_t thr = kNtOutBytes; if (const char* v = getenv("X_NT_MB")) thr = int64_t(atoi(v)) << 20;
+    e.nt_out = out_bytes >= thr;
+#else
+    e.nt_out = out_bytes >= kNtOutBytes;
+#endif
     return glu ? launch_large<true>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
+  }
   // Grids under one round of 256 x 128 tiles take 64 x 64 tiles (4 waves of
   // 32 x 32): 100x2560x2064 35.5 -> 10.5 us, 1000x2048x2064 39.5 -> 16.8 us.
   if (((M + 127) / 128) * ((N + 255) / 256) < 256)
