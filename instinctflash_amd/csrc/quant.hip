@@ -376,6 +376,9 @@ int dispatch_rows(const Src& src, bool vec_ok, int64_t M, int64_t K, uint8_t* q,
     if (nvec <= 64) launch_vec<64, 1>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 128) launch_vec<64, 2>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 256) launch_vec<64, 4>(src, M, K, q, ldq, scale, st);
+    // 6 groups per lane for K <= 3072 (none clamped at K = 3072:
+    // 8192 x 3072 14.6 -> 14.0 us against 8 groups)
+    else if (nvec <= 384) launch_vec<64, 6>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 512) launch_vec<64, 8>(src, M, K, q, ldq, scale, st);
     else if (nvec <= 1024) launch_vec<128, 8>(src, M, K, q, ldq, scale, st);
     else launch_vec<256, 8>(src, M, K, q, ldq, scale, st);

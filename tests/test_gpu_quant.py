@@ -381,7 +381,8 @@ def test_random_wide_range_stress(gpu, oracle_mod, seed):
 # each row a whole block (256 / 512 / 1024 lanes), more rows pack 64-256 lanes per
 # row, K % 8 != 0 takes the generic kernel.
 _FORMS = [(20, 1024), (20, 4096), (20, 8192), (20, 16384), (20, 32768), (20, 1004),
-          (260, 512), (260, 1024), (260, 2048), (260, 4096), (260, 8192), (260, 16384), (260, 32768)]
+          (260, 512), (260, 1024), (260, 2048), (260, 3072), (260, 4096), (260, 8192), (260, 16384),
+          (260, 32768)]
 _SOURCES = ["bf16", "f32", "affine", "affine_col", "affine_bias_gelu", "gelu", "gated_gelu_col", "gated_silu"]
 
 
