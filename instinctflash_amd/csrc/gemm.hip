@@ -509,11 +509,19 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   static_assert(KB == 64 || KB == 128, "stage depth");
   constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
   constexpr int kEpiBytes = kWaves * 32 * kPitch * 4;
-  constexpr int kSmem = STAGES * kStage > kEpiBytes ? STAGES * kStage : kEpiBytes;
-  // the token scales (s_sa) share the CU's LDS with the stage ring
-  static_assert(OCC * (kSmem + BM * 4) <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
-  __shared__ float s_sa[BM];
+  // The 4-wave wide tiles keep the token rows of three stages and the weight
+  // rows of two (a token-row ring one stage deeper than the weight-row ring):
+  // 2 x BN x 128 + 3 x 256 x 128 bytes (160 KB at BN = 256). The token scales
+  // of the epilogue then live in the ring's space after the K loop.
+  constexpr bool kA3 = FM == 4 && KB == 128 && STAGES == 2;
+  constexpr int kWSlot = BN * KB, kASlot = BM * KB;  // bytes of one stage's weight / token rows
+  constexpr int kRing = kA3 ? 2 * kWSlot + 3 * kASlot : STAGES * kStage;
+  constexpr int kSmem = kRing > kEpiBytes + BM * 4 ? kRing : kEpiBytes + BM * 4;
+  // the token scales (s_sa): after the ring, or (kA3) inside it after the K loop
+  constexpr int kLds = kA3 ? kSmem : kSmem + BM * 4;
+  static_assert(OCC * kLds <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+  float* const s_sa = reinterpret_cast<float*>(smem + (kA3 ? kEpiBytes : kSmem));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -611,11 +619,17 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     // < 4 GiB with rows and row strides below 2^24. DMA i of a stage covers
     // tile rows 8 * (wave * kLoads + i) + lrow (weight rows first).
     static_assert(kRowsPerDma == 8, "128-byte rows");
-    const int iw = BN / 8 - wave * kLoads;  // DMAs i < iw of this wave load weight rows
+    // Which 1 KB blocks (8 rows) of a stage wave `wave` fills: with kA3 every
+    // wave takes BN / 32 weight blocks and BM / 32 token blocks (the same
+    // split for all waves, so all wait for the same counts); otherwise blocks
+    // wave * kLoads .. + kLoads - 1 of [weight blocks | token blocks].
+    constexpr int kW4 = BN / 32, kA4 = BM / 32;  // kA3: weight / token DMAs per wave per stage
+    static_assert(!kA3 || kW4 + kA4 == kLoads, "kA3 DMA split");
+    const int iw = kA3 ? kW4 : BN / 8 - wave * kLoads;  // DMAs i < iw of this wave load weight rows
     uint32_t doff[kLoads];                  // per-lane byte offset of DMA i, stage kt0
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int blk = wave * kLoads + i;
+      const int blk = kA3 ? (i < kW4 ? wave * kW4 + i : BN / 8 + wave * kA4 + (i - kW4)) : wave * kLoads + i;
       const int r = blk * 8 + lrow;
       const bool isw = i < iw;
       const uint32_t row = static_cast<uint32_t>(isw ? min(n0 + r, n_last) : min(m0 + (r - BN), m_last));
@@ -623,18 +637,47 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
                 static_cast<uint32_t>(((lpos ^ lrow ^ (blk & 1)) << 4) + kt0 * KB);
     }
     const uint64_t wbase = reinterpret_cast<uintptr_t>(W), abase = reinterpret_cast<uintptr_t>(A);
-    auto dma_one = [&](int kl, int i) {
+    // LDS byte offsets (from smem) of stage kl's weight rows and token rows
+    auto wslot = [&](int kl) -> uint32_t {
+      return kA3 ? (kl & 1) * kWSlot : (kl % STAGES) * kStage;
+    };
+    auto aslot = [&](int kl) -> uint32_t {
+      return kA3 ? 2 * kWSlot + (kl % 3) * kASlot : (kl % STAGES) * kStage + kWSlot;
+    };
+    // DMA i of this wave: weight rows of stage klw (i < iw) or token rows of
+    // stage kla; block blk = wave * kLoads + i lands at row 8 * blk of its stage
+    // (token rows counted from BN).
+    // wdst / adst: this wave's LDS destination bases (lds_base + slot) of the
+    // stages its weight / token DMAs fill, formed once per stage
+    auto dma_one = [&](int klw, int kla, uint32_t wdst, uint32_t adst, int i) {
+      const bool isw = i < iw;  // wave-uniform
       // branch-free wave-uniform choice of the operand base
-      const uint64_t sel = static_cast<uint64_t>(-static_cast<int64_t>(i < iw));
+      const uint64_t sel = static_cast<uint64_t>(-static_cast<int64_t>(isw));
       const uint8_t* base = reinterpret_cast<const uint8_t*>(abase ^ ((wbase ^ abase) & sel));
-      dma16s(base, doff[i] + static_cast<uint32_t>(kl) * KB, lds_base + (kl % STAGES) * kStage + i * 1024);
+      const int kl = isw ? klw : kla;
+      dma16s(base, doff[i] + static_cast<uint32_t>(kl) * KB, (isw ? wdst : adst) + i * 1024);
+    };
+    // bases such that DMA i lands at base + i * 1024
+    const uint32_t smem_off = lds_offset(smem);
+    auto wdst_of = [&](int kl) {
+      return __builtin_amdgcn_readfirstlane(kA3 ? smem_off + wslot(kl) + wave * kW4 * 1024 : lds_base + wslot(kl));
+    };
+    auto adst_of = [&](int kl) {
+      return __builtin_amdgcn_readfirstlane(kA3 ? smem_off + aslot(kl) + (wave * kA4 - kW4) * 1024
+                                                : lds_base + aslot(kl) - kWSlot);
     };
     // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (2kFN+2j, 2kFN+2j+1)
     v4i fr[2][kRd];
-    auto read_one = [&](const uint8_t* base, v4i* f, int h, int r) {
-      const int row = r < 2 * kFN ? wn * (32 * kFN) + (r >> 1) * 32 + frow : BN + wm * kWT + ((r - 2 * kFN) >> 1) * 32 + frow;
-      f[r] = ld16(base + S::off(row, 4 * h + 2 * fhalf + (r & 1)));
+    // wp / ap: the stage's weight-row and token-row slots
+    auto read_one = [&](const uint8_t* wp, const uint8_t* ap, v4i* f, int h, int r) {
+      const int ch = 4 * h + 2 * fhalf + (r & 1);
+      if (r < 2 * kFN) {
+        f[r] = ld16(wp + S::off(wn * (32 * kFN) + (r >> 1) * 32 + frow, ch));
+      } else {
+        f[r] = ld16(ap + S::off(wm * kWT + ((r - 2 * kFN) >> 1) * 32 + frow, ch));
+      }
     };
+
     auto mfma_one = [&](const v4i* f, int m) {
       const int i = m / kFM, j = m % kFM;
       acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[2 * kFN + 2 * j], f[2 * kFN + 2 * j + 1]), acc[i][j]);
@@ -653,48 +696,101 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     };
-    // prologue: stages 0 .. STAGES-1 in flight, stage 0 landed, its half-0 fragments read
+    if constexpr (kA3) {
+      // Token rows three stages deep, weight rows two. Stage kt's second half
+      // issues the weight rows of stage kt+2 and the token rows of stage kt+3
+      // (weight DMAs first), both into the slots stage kt has just freed; the
+      // barrier of stage kt then needs everything but the newest token rows
+      // (stage kt+2), which stay in flight: token rows get two stages of lead.
+      // Prologue order per wave: W0 A0 W1 A1 A2 (each its own DMAs only).
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) dma_one(0, i);
+      for (int s = 0; s < 3; ++s) {
+        const uint32_t wd = wdst_of(s), ad = adst_of(s);
 #pragma unroll
-    for (int s = 1; s < STAGES; ++s)
-      if (s < nk) {
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) dma_one(s, i);
+        for (int i = 0; i < kLoads; ++i) {
+          if (i < iw) {
+            if (s < 2 && s < nk) dma_one(s, 0, wd, ad, i);
+          } else if (s < nk) {
+            dma_one(0, s, wd, ad, i);
+          }
+        }
       }
-    if (nk >= STAGES) wait_vmcnt<(STAGES - 1) * kLoads>();
-    else wait_vmcnt<0>();
+      if (nk >= 3) wait_vmcnt<kW4 + 2 * kA4>();  // this wave's W1 A1 A2 may stay in flight
+      else if (nk == 2) wait_vmcnt<kLoads>();
+      else wait_vmcnt<0>();
+    } else {
+      // prologue: stages 0 .. STAGES-1 in flight, stage 0 landed
+#pragma unroll
+      for (int s = 0; s < STAGES; ++s)
+        if (s < nk) {
+          const uint32_t wd = wdst_of(s), ad = adst_of(s);
+#pragma unroll
+          for (int i = 0; i < kLoads; ++i) dma_one(s, s, wd, ad, i);
+        }
+      if (nk >= STAGES) wait_vmcnt<(STAGES - 1) * kLoads>();
+      else wait_vmcnt<0>();
+    }
     sync();
 #pragma unroll
-    for (int r = 0; r < kRd; ++r) read_one(smem, fr[0], 0, r);
-    auto stage = [&](int kt, auto dma_tag) {
-      constexpr bool kDma = decltype(dma_tag)::value;  // stage kt + STAGES exists
-      const uint8_t* cur = smem + (kt % STAGES) * kStage;
-      const uint8_t* nxt = smem + ((kt + 1) % STAGES) * kStage;  // after the last stage: a settled slot, unused
+    for (int r = 0; r < kRd; ++r) read_one(smem + wslot(0), smem + aslot(0), fr[0], 0, r);  // stage 0's half 0
+    // kDmaW: stage kt + STAGES exists (its weight rows, or with kA3 its rows
+    // of both operands in the ring's form); kDmaA (kA3): stage kt + 3 exists.
+    auto stage = [&](int kt, auto dmaw_tag, auto dmaa_tag) {
+      constexpr bool kDmaW = decltype(dmaw_tag)::value;
+      constexpr bool kDmaA = decltype(dmaa_tag)::value;
+      const uint8_t* wcur = smem + wslot(kt);
+      const uint8_t* acur = smem + aslot(kt);
+      const uint8_t* wnxt = smem + wslot(kt + 1);  // after the last stage: a settled slot, unused
+      const uint8_t* anxt = smem + aslot(kt + 1);
       wait_lgkm0();
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
         if (m < kMF) mfma_one(fr[0], m);
-        read_one(cur, fr[1], 1, m);
+        read_one(wcur, acur, fr[1], 1, m);
       }
       interleave();
       wait_lgkm0();
-      if (kDma || kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();  // stages up to kt+STAGES-1 issued
-      else if (kt + 1 < nk) wait_vmcnt<0>();
+      if constexpr (kA3) {
+        // stage kt+1 landed; the token rows of stage kt+2 may stay in flight
+        if (kt + 2 < nk) wait_vmcnt<kA4>();
+        else if (kt + 1 < nk) wait_vmcnt<0>();
+      } else {
+        if (kDmaW || kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();  // stages up to kt+STAGES-1 issued
+        else if (kt + 1 < nk) wait_vmcnt<0>();
+      }
       sync();
+      // DMA destinations: kA3 weight rows of stage kt+2 and token rows of
+      // stage kt+3 (both the slots of stage kt); otherwise stage kt+STAGES
+      const uint32_t wd = wdst_of(kA3 ? kt + 2 : kt + STAGES);
+      const uint32_t ad = adst_of(kA3 ? kt + 3 : kt + STAGES);
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
         if (m < kMF) mfma_one(fr[1], m);
-        read_one(nxt, fr[0], 0, m);
-        if constexpr (kDma) {
-          if (m < kLoads) dma_one(kt + STAGES, m);
+        read_one(wnxt, anxt, fr[0], 0, m);
+        if (m < kLoads) {
+          if constexpr (kA3) {
+            if (m < iw) {
+              if constexpr (kDmaW) dma_one(kt + 2, 0, wd, ad, m);
+            } else {
+              if constexpr (kDmaA) dma_one(0, kt + 3, wd, ad, m);
+            }
+          } else if constexpr (kDmaW) {
+            dma_one(kt + STAGES, kt + STAGES, wd, ad, m);
+          }
         }
       }
       interleave();
     };
+    using std::false_type;
+    using std::true_type;
     int kt = 0;
-    for (; kt + STAGES < nk; ++kt) stage(kt, std::true_type{});
-    for (; kt < nk; ++kt) stage(kt, std::false_type{});
+    if constexpr (kA3) {
+      for (; kt + 3 < nk; ++kt) stage(kt, true_type{}, true_type{});
+      for (; kt + 2 < nk; ++kt) stage(kt, true_type{}, false_type{});
+    } else {
+      for (; kt + STAGES < nk; ++kt) stage(kt, true_type{}, false_type{});
+    }
+    for (; kt < nk; ++kt) stage(kt, false_type{}, false_type{});
     wait_vmcnt<0>();  // no DMA may still write LDS when the epilogue reuses it
   } else {
 #pragma unroll
@@ -778,6 +874,11 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
   uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
   if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
+  if constexpr (kA3) {
+    // s_sa overlays the ring: every wave must be done reading its last stage
+    asm volatile("" ::: "memory");
+    __syncthreads();
+  }
   for (int t = tid; t < BM; t += kWaves * 64) s_sa[t] = epi_sa(e, min(m0 + t, e.M - 1));
   asm volatile("" ::: "memory");
   __syncthreads();
