@@ -261,205 +261,6 @@ def measure_producers(dev, launches=32):
     return res
 
 
-def measure_engine(dev, reps=5):
-    """The pi05 action expert end to end on these kernels (reference
-    engines/pi05/engine.py:212-245): 10 Euler steps x 18 layers over an
-    800-row prefix cache, random weights of the architecture, one captured
-    graph; ms per 50-action chunk (median of `reps` replays)."""
-    import torch
-    from instinctflash_amd.pi05 import Pi05Expert, random_weights
-    w = random_weights(dev, layers=18, steps=10, seed=0)
-    eng = Pi05Expert(w, dev, smax=832)
-    g = torch.Generator().manual_seed(1)
-    eng.kc[:, :800] = torch.randn(18, 800, 1, 256, generator=g).half().to(dev)
-    eng.vc[:, :800] = torch.randn(18, 800, 1, 256, generator=g).half().to(dev)
-    eng.set_prefix(800)
-    eng.noise.copy_(torch.randn(eng.chunk, 32, generator=g))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        eng.forward()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = capture(lambda i: eng.forward(), 1, side)
-    time_graph(graph)
-    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    launches = 10 * (2 + 18 * 8)
-    _log(f"[bench] pi05 expert: {ms:.3f} ms per 50-action chunk ({launches} kernels + torch addmm)")
-    return {"workload": "pi05 action expert, 10 steps x 18 layers, prefix 800, chunk 50 (random weights)",
-            "ms_per_chunk": round(ms, 4), "kernels_per_chunk": launches}
-
-
-def measure_prefix(dev, layers=4, reps=5):
-    """The prefix stacks that define C3 (pi05 PaliGemma, 816 rows) and C4 (VLA4
-    Qwen2.5, 1024 rows) end to end on these kernels (instinctflash_amd/
-    prefix.py; reference engines/pi05/engine.py:192-216, engines/vla4/
-    engine.py:114-139): `layers` decoder layers of random weights captured in
-    one graph; µs per layer and the layer's FP8 GEMM TFLOP/s."""
-    import torch
-    from instinctflash_amd.prefix import PI05_PREFIX, VLA4_PREFIX, PrefixStack, random_prefix_weights
-    out = {}
-    for cfg, M in ((PI05_PREFIX, 816), (VLA4_PREFIX, 1024)):
-        st = PrefixStack(cfg, random_prefix_weights(cfg, layers, dev, seed=0), dev, smax=M)
-        st.set_prefix(M)
-        x = torch.randn(M, cfg.D, generator=torch.Generator().manual_seed(1)).to(dev)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            st.forward(x, M)
-        torch.cuda.current_stream().wait_stream(side)
-        g = capture(lambda i: st.forward(x, M), 1, side)
-        time_graph(g)
-        ms = sorted(time_graph(g)[0] for _ in range(reps))[reps // 2]
-        flops = 2 * M * cfg.D * (cfg.qkv_n + cfg.HQ * cfg.HD + 3 * cfg.FF)  # qkv, o, gate|up, down
-        us = ms * 1e3 / layers
-        out[cfg.name] = {"rows": M, "layers": layers, "us_per_layer": round(us, 2),
-                         "gemm_tflops": round(flops / us / 1e6, 1),
-                         "kernels_per_layer": 9}
-        _log(f"[bench] {cfg.name}: {us:.1f} us per layer ({flops / us / 1e6:.0f} TFLOP/s of FP8 GEMM)")
-        del st, g
-        torch.cuda.empty_cache()
-    return out
-
-
-def measure_pi05_full(dev, reps=5):
-    """The whole pi05 forward on these kernels (instinctflash_amd/pi05_engine.py;
-    reference engines/pi05/engine.py:151-245): 3 camera views through the
-    27-layer SigLIP tower and the projector, the 18-layer Gemma-2B prefix over
-    816 rows (768 image + 48 prompt rows: config C3's M), and 10 Euler steps of
-    the 18-layer action expert, one captured graph, random weights; ms per
-    50-action chunk (the reference publishes 51.85 ms for this forward on
-    Jetson Thor, README.md:38)."""
-    import torch
-    from instinctflash_amd.pi05_engine import LM_D, Pi05Engine, random_pi05_weights
-    w = random_pi05_weights(dev, seed=0)
-    eng = Pi05Engine(w, 3, dev, max_prompt=48)
-    g = torch.Generator().manual_seed(1)
-    eng.img.copy_(torch.rand(3, 3, 224, 224, generator=g) * 2 - 1)
-    eng.expert.noise.copy_(torch.randn(eng.expert.chunk, 32, generator=g))
-    M = eng.set_prompt(torch.randn(48, LM_D, generator=g).to(dev))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        eng.forward(M)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = capture(lambda i: eng.forward(M), 1, side)
-    time_graph(graph)
-    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    _log(f"[bench] pi05 full forward: {ms:.3f} ms per chunk (3 views, {M} prefix rows)")
-    out = {"workload": "pi05: 3 views x SigLIP 27 layers, Gemma-2B prefix 18 layers x 816 rows, expert 10 steps x 18 "
-                       "layers, chunk 50 (random weights)", "ms_per_chunk": round(ms, 3),
-           "reference_published_ms": {"value": 51.85, "hardware": "Jetson Thor", "source": "README.md:38"}}
-    del eng, w, graph
-    torch.cuda.empty_cache()
-    return out
-
-
-def measure_vla4_full(dev, reps=5):
-    """The LingBot-VLA-4B forward on these kernels (instinctflash_amd/
-    vla4_engine.py; reference engines/vla4/engine.py:109-177): the 36-layer
-    Qwen2.5 prefix over 192 vision + 48 prompt rows and 10 Euler steps of the
-    36-layer expert over the 51 suffix rows, one captured graph, random weights;
-    ms per 50-action chunk (the vision embeddings are an input, as upstream,
-    where the model's own bf16 tower makes them)."""
-    import torch
-    from instinctflash_amd.vla4_engine import D, STATE_DIM, VISION_TOKENS, Vla4Engine, random_vla4_weights
-    eng = Vla4Engine(random_vla4_weights(dev, seed=0), dev)
-    g = torch.Generator().manual_seed(1)
-    eng.vis.copy_(torch.randn(VISION_TOKENS, D, generator=g))
-    eng.state.copy_(torch.randn(1, STATE_DIM, generator=g))
-    eng.noise.copy_(torch.randn(eng.chunk, STATE_DIM, generator=g))
-    M = eng.set_prompt(torch.randn(48, D, generator=g).to(dev))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        eng.forward(M)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = capture(lambda i: eng.forward(M), 1, side)
-    time_graph(graph)
-    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    _log(f"[bench] LingBot-VLA-4B forward: {ms:.3f} ms per chunk ({M} prefix rows)")
-    out = {"workload": "LingBot-VLA-4B: Qwen2.5 prefix 36 layers x 240 rows, expert 10 steps x 36 layers x 51 rows "
-                       "(random weights; vision embeddings as input)", "ms_per_chunk": round(ms, 3),
-           "reference_published_ms": {"value": 221.53, "hardware": "Jetson Thor", "source": "README.md:34",
-                                      "note": "whole prediction, bf16 vision tower included"}}
-    del eng, graph
-    torch.cuda.empty_cache()
-    return out
-
-
-def measure_groot(dev, reps=5):
-    """The GR00T N1.7 action head end to end on these kernels (instinctflash_amd/
-    groot.py; reference engines/groot_n17/engine.py:92-200): LayerNorm + 4 VLSA
-    blocks over 256 backbone rows, the 16 cross K/V projections, and 4 flow
-    steps of the 32-block DiT over 41 rows (the C2 MLP in every block), random
-    weights of the architecture, one captured graph; ms per inference."""
-    import torch
-    from instinctflash_amd.groot import ACT_DIM, HORIZON, VL_D, GrootHead, random_groot_weights
-    w = random_groot_weights(dev, seed=0)
-    head = GrootHead(w, dev, max_seq=256)
-    g = torch.Generator().manual_seed(1)
-    n = 256
-    head.set_inputs(torch.randn(n, VL_D, generator=g).to(dev), (torch.rand(n, generator=g) < 0.7).to(dev),
-                    torch.ones(n, dtype=torch.bool, device=dev), torch.randn(ACT_DIM, generator=g).to(dev),
-                    torch.randn(HORIZON, ACT_DIM, generator=g).to(dev))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        head.forward(n)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = capture(lambda i: head.forward(n), 1, side)
-    time_graph(graph)
-    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    _log(f"[bench] GR00T N1.7 head: {ms:.3f} ms per inference")
-    out = {"workload": "GR00T N1.7 action head: 4 VLSA blocks x 256 rows, 16 cross K/V, 4 steps x 32 DiT blocks "
-                       "x 41 rows (random weights)", "ms_per_inference": round(ms, 4)}
-    del head, w, graph
-    torch.cuda.empty_cache()
-    return out
-
-
-def measure_wan(dev, blocks=4, reps=5):
-    """The LingBot-VA (Wan2.2 5B) transformer blocks on these kernels
-    (instinctflash_amd/wan_block.py; reference engines/wan_va/engine.py:
-    205-245) at the engine's largest forward (2 batches x 512 tokens, 1024 rows
-    of the C5 projections) over a 4096-slot KV pool with 2560 live slots and 512
-    text rows: `blocks` blocks captured in one graph; µs per block and its FP8
-    GEMM TFLOP/s."""
-    import torch
-    from instinctflash_amd.wan_block import WanStack, random_wan_blocks
-    B, T, S, live = 2, 512, 4096, 2560
-    st = WanStack(random_wan_blocks(blocks, dev, seed=0), dev, pool_slots=S, max_tokens=T, max_batch=B)
-    g = torch.Generator().manual_seed(1)
-    D, FF = st.D, st.FF
-    st.live[:live].copy_(torch.arange(live, dtype=torch.int32))
-    st.n_live.fill_(live)
-    st.slots[:T].copy_(torch.arange(live - T, live, dtype=torch.int32))
-    st.pos[:T].copy_(torch.stack([torch.arange(T) // 256, (torch.arange(T) // 16) % 16, torch.arange(T) % 16], 1))
-    st.mod_index.copy_((torch.randint(0, 2, (B * T,), generator=g) * 6).int())
-    block_mod = (torch.randn(blocks, 2, 6, D, generator=g) * 0.1).to(dev)
-    head_mod = (torch.randn(2, 6, D, generator=g) * 0.1).to(dev)
-    st.prepare_text(torch.randn(B, st.TEXT, D, generator=g).to(dev))
-    x = torch.randn(B * T, D, generator=g).to(dev)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        st.forward(B, T, block_mod, head_mod, x=x)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = capture(lambda i: st.forward(B, T, block_mod, head_mod, x=x), 1, side)
-    time_graph(graph)
-    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
-    us = ms * 1e3 / blocks
-    R = B * T
-    flops = 2 * R * D * (3 * D + D + D + D + 2 * FF)  # qkv, o, cross q, cross o, ff1, ff2
-    _log(f"[bench] Wan blocks: {us:.1f} us per block ({flops / us / 1e6:.0f} TFLOP/s of FP8 GEMM)")
-    out = {"workload": f"LingBot-VA Wan2.2 5B blocks, {B} x {T} tokens, {live} live pool slots, 512 text rows "
-                       "(random weights)", "blocks": blocks, "us_per_block": round(us, 2),
-           "gemm_tflops": round(flops / us / 1e6, 1)}
-    del st, graph
-    torch.cuda.empty_cache()
-    return out
-
-
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -680,12 +481,6 @@ def main():
     }
     if not args.no_others:
         out["producers"] = measure_producers(dev)
-        out["engine"] = measure_engine(dev)
-        out["prefix"] = measure_prefix(dev)
-        out["pi05_full"] = measure_pi05_full(dev)
-        out["vla4_full"] = measure_vla4_full(dev)
-        out["groot"] = measure_groot(dev)
-        out["wan"] = measure_wan(dev)
     if not args.no_cpu:
         for key in order:
             _log(f"[bench] CPU baseline {key} (reference CPU FP8 path)")

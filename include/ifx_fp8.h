@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define IFX_ABI_VERSION 1
+#define IFX_ABI_VERSION 2
 
 /* status codes (negative = rejected before launch) */
 #define IFX_OK 0

@@ -1773,12 +1773,7 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
   }
   if (big_path(M, K)) {
     const int64_t out_bytes = M * (glu ? N / 2 : N) * static_cast<int64_t>(sizeof(uint16_t));
-#ifdef X_ENV
-    int64_t thr = kNtOutBytes; if (const char* v = getenv("X_NT_MB")) thr = int64_t(atoi(v)) << 20;
-    e.nt_out = out_bytes >= thr;
-#else
     e.nt_out = out_bytes >= kNtOutBytes;
-#endif
     return glu ? launch_large<true>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
                : launch_large<false>(A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
   }
@@ -1848,10 +1843,14 @@ size_t ifx_quant_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epil
   return ql_workspace(M, N, K, epilogue, scale_mode).total;
 }
 
-int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw, const float* sw,
-                     const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
-                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
-                     size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// Contract checks of ifx_quant_linear that do not involve the workspace, shared
+// with ifx_quant_linear_noalloc so that a rejected call launches nothing.
+int check_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw, const float* sw,
+                       const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
+                       void* out, int64_t ldo, int64_t M, int64_t N, int64_t K) {
   if (scale_mode != IFX_SCALE_ROW && scale_mode != IFX_SCALE_TENSOR) return IFX_ERR_INVALID;
   if (epilogue & IFX_EPI_SCALAR_SA) return IFX_ERR_INVALID;  // the scale is computed here
   const int rc = check_linear(w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
@@ -1860,10 +1859,23 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
   if (M == 0) return IFX_OK;
   if (!x) return IFX_ERR_INVALID;
   if (!aligned16(x) || ldx % 8 != 0) return IFX_ERR_ALIGN;
+  if (scale_mode == IFX_SCALE_TENSOR && ldx != K) return IFX_ERR_UNSUPPORTED;
+  return IFX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, int64_t ldw, const float* sw,
+                     const float* bias, const void* residual, int64_t ldr, const void* gate, int epilogue,
+                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, float* a_scale, void* workspace,
+                     size_t ws_bytes, void* stream) {
+  const int rc = check_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo,
+                                    M, N, K);
+  if (rc != IFX_OK || M == 0) return rc;
   // the stand-alone quantizer into the workspace, then the GEMM
   const QlWorkspace ql = ql_workspace(M, N, K, epilogue, scale_mode);
   if (!workspace || ws_bytes < ql.total || (reinterpret_cast<uintptr_t>(workspace) & 255u)) return IFX_ERR_WORKSPACE;
-  if (scale_mode == IFX_SCALE_TENSOR && ldx != K) return IFX_ERR_UNSUPPORTED;
   uint8_t* base = static_cast<uint8_t*>(workspace);
   void* gws = base;
   uint8_t* q = base + ql.gemm;
@@ -1948,13 +1960,11 @@ int ifx_quant_linear_noalloc(const void* x, int64_t ldx, int scale_mode, const v
                              const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                              int64_t K, float* a_scale, void* stream) {
   if (M < 0 || N <= 0 || K <= 0) return IFX_ERR_INVALID;
-  if (M == 0)  // nothing to launch; let ifx_quant_linear validate the rest
-    return ifx_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N,
-                            K, a_scale, nullptr, 0, stream);
-  if (scale_mode != IFX_SCALE_ROW && scale_mode != IFX_SCALE_TENSOR) return IFX_ERR_INVALID;
+  // every contract check before the clear below: a rejected call launches nothing
+  int rc = check_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
+  if (rc != IFX_OK || M == 0) return rc;
   const size_t need = ql_workspace(M, N, K, epilogue, scale_mode).total;
   if (need > kScratchBytes) return IFX_ERR_SCRATCH;
-  int rc = IFX_OK;
   void* ws = scratch_ptr(&rc);
   if (!ws) return rc;
   // The ticket header must read zero. Every call leaves it so, but a call that

@@ -80,3 +80,19 @@ def wan_qkv(raw, q_out, *, heads, head_dim, tokens, k_pool=None, v_pool=None, sl
         _ptr(bias), _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(inv_freq), _ptr(pos) if inv_freq is not None else None,
         ldpos, _ptr(sections) if inv_freq is not None else None, _ptr(q_out), sq, _ptr(k_pool), sk_b, sk_s,
         _ptr(v_pool), sv_b, sv_s, _ptr(slots), _OUT[q_out.dtype], rows, T, H, HD, _stream(dev)), "ifx_wan_qkv")
+
+
+def wan_rope_tables(head_dim=128, theta=10000.0, device=None):
+    """3-D rotary frequency tables for ``wan_qkv`` (reference
+    engines/wan_va/weights.py:76-84): the head's channel pairs split into frame /
+    height / width sections of HD - 2 (HD // 3), HD // 3 and HD // 3 channels,
+    each with its own ladder theta^(-2i / d). Returns (inv_freq float32 [HD / 2],
+    sections int32 [HD / 2], 0 = frame, 1 = height, 2 = width)."""
+    hw = head_dim // 3
+    dims = (head_dim - 2 * hw, hw, hw)
+    freqs, secs = [], []
+    for s, d in enumerate(dims):
+        i = torch.arange(d // 2, dtype=torch.float64)
+        freqs.append(theta ** (-2.0 * i / d))
+        secs.append(torch.full((d // 2,), s, dtype=torch.int32))
+    return torch.cat(freqs).float().to(device), torch.cat(secs).to(device)

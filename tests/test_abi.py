@@ -40,7 +40,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.ifx_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.ifx_abi_version() == _lib.ABI_VERSION == 2
     for code in (_lib.OK, _lib.ERR_INVALID, _lib.ERR_ALIGN, _lib.ERR_WORKSPACE, _lib.ERR_UNSUPPORTED):
         assert lib.ifx_status_string(code)
     macro = dict(re.findall(r"#define (IFX_(?:ERR_\w+|OK|EPI_\w+|ACT_\w+|DTYPE_\w+|ABI_VERSION))\s+\(?(-?\d+)\)?",
@@ -117,6 +117,17 @@ def test_contract_violations_rejected_before_launch(lib):
     assert ql(64, _lib.SCALE_ROW, 0, 100, 64) == _lib.ERR_WORKSPACE
     assert ql(64, _lib.SCALE_ROW, 0, 16, 64) == _lib.ERR_WORKSPACE
     assert ql(64, _lib.SCALE_ROW, 0, 0, 64) == _lib.OK
+    # the no-allocation variant runs the same checks before its scratch clear,
+    # so a rejected call launches nothing (these return without touching a GPU)
+    qn = lambda x, ldx, mode, epi, M, K: lib.ifx_quant_linear_noalloc(  # noqa: E731
+        x, ldx, mode, fake, 64, fake, None, None, 0, None, epi, fake, 64, M, 64, K, None, None)
+    assert qn(P(0x1001), 64, _lib.SCALE_ROW, 0, 16, 64) == _lib.ERR_ALIGN
+    assert qn(fake, 60, _lib.SCALE_ROW, 0, 16, 48) == _lib.ERR_ALIGN
+    assert qn(None, 64, _lib.SCALE_ROW, 0, 16, 64) == _lib.ERR_INVALID
+    assert qn(fake, 64, 2, 0, 16, 64) == _lib.ERR_INVALID
+    assert qn(fake, 64, _lib.SCALE_ROW, 1 << 13, 16, 64) == _lib.ERR_INVALID
+    assert qn(fake, 16, _lib.SCALE_TENSOR, 0, 16, 32) == _lib.ERR_INVALID
+    assert qn(fake, 128, _lib.SCALE_TENSOR, 0, 16, 64) == _lib.ERR_UNSUPPORTED
     assert lib.ifx_dequant_rows(fake, 0, 64, 1, 64, None, None, None, fake, 9, 64, None) == _lib.ERR_INVALID
     assert lib.ifx_dequant_rows(fake, 7, 64, 1, 64, None, None, None, fake, 0, 64, None) == _lib.ERR_INVALID
 

@@ -179,7 +179,7 @@ def test_wan_rope_tables_sections_and_ladders():
     # 3-D rotary of the Wan blocks (reference engines/wan_va/weights.py:76-84):
     # 128-dim heads split their 64 channel pairs 22 / 21 / 21 over frame, height
     # and width; each section's ladder starts at 1 and falls by theta^(-2/d)
-    from instinctflash_amd.wan_block import wan_rope_tables
+    from instinctflash_amd.kernels.wan import wan_rope_tables
     inv, sec = wan_rope_tables(128, 10000.0)
     assert inv.dtype == torch.float32 and sec.dtype == torch.int32 and inv.numel() == sec.numel() == 64
     assert [int((sec == s).sum()) for s in range(3)] == [22, 21, 21]

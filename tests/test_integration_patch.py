@@ -68,3 +68,27 @@ def test_kernel_seam_modules_export_engine_names():
         m = importlib.import_module(f"instinctflash_amd.kernels.{mod}")
         missing = [n for n in names if not hasattr(m, n)]
         assert not missing, f"instinctflash_amd.kernels.{mod} lacks {missing}"
+
+
+REF = Path("/root/reference")
+GATE_FILES = ("instinctflash/kernels/__init__.py", "instinctflash/passes/contract.py",
+              "instinctflash/passes/generic/engine_offload.py", "instinctflash/runtime/engine_backend.py")
+
+
+def test_patch_applies_to_the_reference_gate_files(tmp_path):
+    # Copies the four gate files out of the reference tree (read only) and
+    # dry-runs the patch on the copies, so drift in either side fails here.
+    import shutil
+    import subprocess
+
+    import pytest
+    if not all((REF / f).is_file() for f in GATE_FILES):
+        pytest.skip("reference tree not present (only in the build container)")
+    for f in GATE_FILES:
+        dst = tmp_path / f
+        dst.parent.mkdir(parents=True, exist_ok=True)
+        shutil.copyfile(REF / f, dst)
+    res = subprocess.run(["git", "apply", "--check", "-p1", str(PATCH)], cwd=tmp_path, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    res = subprocess.run(["patch", "--dry-run", "-p1", "-i", str(PATCH)], cwd=tmp_path, capture_output=True, text=True)
+    assert res.returncode == 0, res.stdout + res.stderr
