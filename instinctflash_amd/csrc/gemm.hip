@@ -1190,6 +1190,7 @@ struct SkinnyPlan {
   int64_t kss;     // K steps per slice
   int waves;       // waves per workgroup (4, 8 or 16)
   int tsplit;      // workgroups along the tokens per group (each owns mb blocks)
+  int rhalves;     // workgroups along the group's 16 weight rows (2: 8 rows each)
   size_t ws_bytes; // workspace (tickets + partials) when ksplit > 1
 };
 
@@ -1229,6 +1230,12 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
     p.tsplit = 2;
     p.mb = 2;
   }
+  // Too few row groups to reach every CU (one 16-token block, unsplit K): two
+  // workgroups per group, each streaming 8 of its 16 weight rows (the other 8
+  // MFMA rows are zeros and their outputs are not stored). The matrix cores
+  // are idle here anyway; the weight stream spreads over twice the CUs.
+  p.rhalves = 1;
+  if (p.ksplit == 1 && p.mb == 1 && p.tsplit == 1 && p.nbw == 1 && p.groups * 2 <= kSkMaxGroups) p.rhalves = 2;
   // Enough waves that every wave has at most kSkUnroll K steps of its slice
   // (one batch of loads in flight); 16 waves leave 128 VGPRs each, enough
   // for one 16 x 16 block only.
@@ -1245,7 +1252,7 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
 // TILED: w is in the layout of ifx_fp8_pack_skinny (2 KB tile per 16-row block
 // and 128-byte K step, zero-padded in K), so each weight load instruction of a
 // wave reads 1 KB of contiguous memory.
-template <int MB, int NBW, int WAVES, bool TILED>
+template <int MB, int NBW, int WAVES, bool TILED, int RH = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
                                                           const uint8_t* __restrict__ W, int64_t ldw,
                                                           int64_t K, Epi e, SkSplit sp) {
@@ -1255,11 +1262,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t groups = e.N / (16 * NBW);
-  const int64_t grp = static_cast<int64_t>(blockIdx.x) % groups;
-  const int slice = static_cast<int>(static_cast<int64_t>(blockIdx.x) / groups);
+  // RH > 1: RH workgroups split the group's 16 weight rows (16 / RH each)
+  const int rh = RH == 1 ? 0 : static_cast<int>(blockIdx.x % RH);
+  const int64_t bx = static_cast<int64_t>(blockIdx.x) / RH;
+  const int64_t grp = bx % groups;
+  const int slice = static_cast<int>(bx / groups);
   const int64_t nrow0 = grp * (16 * NBW);
   const int frow = lane & 15;
   const int g = lane >> 4;
+  // this lane's weight row is streamed here / its output rows are stored here
+  const bool wmine = RH == 1 || frow / (16 / RH) == rh;
+  const bool omine = RH == 1 || (4 * g) / (16 / RH) == rh;
   const int64_t ksteps = (K + kBK - 1) / kBK;
   const int64_t s_begin = slice * sp.kss;
   const int64_t s_end = min(s_begin + sp.kss, ksteps);
@@ -1322,12 +1335,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #pragma unroll
       for (int b = 0; b < NBW; ++b) {
         if constexpr (TILED) {
-          const bool in = s < s_end;
+          const bool in = s < s_end && wmine;
           const uint8_t* p = W + ((grp * NBW + b) * ksteps + s) * 2048 + lane * 16;
           wf[u][b] = cat8(in ? ld16_nt(p) : v4i{0, 0, 0, 0}, in ? ld16_nt(p + 1024) : v4i{0, 0, 0, 0});
         } else {
           const uint8_t* p = wrow[b] + s * kBK;
-          wf[u][b] = cat8(lo ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
+          wf[u][b] = cat8(lo && wmine ? ld16_nt(p) : v4i{0, 0, 0, 0}, hi && wmine ? ld16_nt(p + 16) : v4i{0, 0, 0, 0});
         }
       }
 #pragma unroll
@@ -1402,7 +1415,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
     }
   }
 
-  if (wave < MB && m_epi < e.M) {
+  if (wave < MB && m_epi < e.M && omine) {
     float y[4];
     if constexpr (NBW == 2) {
 #pragma unroll
@@ -1499,7 +1512,17 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
 template <int MB, int NBW, int WAVES>
 void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
                      const Epi& e, const SkSplit& sp, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit), static_cast<unsigned>(p.tsplit)), block(WAVES * 64);
+  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit * p.rhalves), static_cast<unsigned>(p.tsplit)),
+      block(WAVES * 64);
+  if constexpr (MB == 1 && NBW == 1) {
+    if (p.rhalves == 2) {
+      if (e.flags & IFX_EPI_W_TILED)
+        hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, true, 2>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
+      else
+        hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, false, 2>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
+      return;
+    }
+  }
   if (e.flags & IFX_EPI_W_TILED)
     hipLaunchKernelGGL((gemm_skinny<MB, NBW, WAVES, true>), grid, block, 0, st, a, lda, w, ldw, K, e, sp);
   else
