@@ -261,6 +261,37 @@ def measure_producers(dev, launches=32):
     return res
 
 
+def measure_pi05(dev, reps=5):
+    """The whole pi05 prediction on these kernels (instinctflash_amd/
+    pi05_forward.py; the model of reference engines/pi05/engine.py): 3 camera
+    views through the 27-layer SigLIP tower and the projector, the 18-layer
+    Gemma-2B prefix over 816 rows (768 image + 48 prompt rows: config C3's M),
+    and 10 Euler steps of the 18-layer action expert over the 50-action chunk,
+    random weights, one captured graph; ms per chunk (median of `reps`
+    replays). The reference publishes 51.85 ms for this forward on Jetson Thor
+    (README.md:38)."""
+    import torch
+    from instinctflash_amd.pi05_forward import Pi05Dims, Pi05Forward, random_pi05
+    d = Pi05Dims()
+    fwd = Pi05Forward(random_pi05(d, dev, seed=0), dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    fwd.set_inputs(torch.rand(d.views, 3, 224, 224, generator=g, device=dev) * 2 - 1,
+                   torch.randn(d.max_prompt, d.lm_d, generator=g, device=dev),
+                   torch.randn(d.chunk, d.action, generator=g, device=dev))
+    graph = fwd.capture()
+    time_graph(graph)
+    ms = sorted(time_graph(graph)[0] for _ in range(reps))[reps // 2]
+    launches = sum(1 for l in fwd.schedule if l.kind != "torch")
+    _log(f"[bench] pi05 forward: {ms:.3f} ms per chunk ({launches} HIP launches + {len(fwd.schedule) - launches} torch ops)")
+    out = {"workload": "pi05: 3 views x SigLIP 27 layers, Gemma-2B prefix 18 layers x 816 rows, expert 10 steps x 18 "
+                       "layers, chunk 50 (random weights, one HIP graph)", "ms_per_chunk": round(ms, 3),
+           "launches": len(fwd.schedule),
+           "reference_published_ms": {"value": 51.85, "hardware": "Jetson Thor", "source": "README.md:38"}}
+    del fwd, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def probe(wl, dev, launches=20, copy_bytes=1 << 30):
     """Counter-run helper: the dominant kernel alone, then a plain copy of known
     size (the calibration for FETCH_SIZE / WRITE_SIZE), each `launches` times."""
@@ -481,6 +512,7 @@ def main():
     }
     if not args.no_others:
         out["producers"] = measure_producers(dev)
+        out["pi05_forward"] = measure_pi05(dev)
     if not args.no_cpu:
         for key in order:
             _log(f"[bench] CPU baseline {key} (reference CPU FP8 path)")
