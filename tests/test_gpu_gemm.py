@@ -599,3 +599,23 @@ def test_wide_192_row_tiles(gpu, oracle_mod, M, N, K, act, resgate):
     res = torch.randn((M, N), generator=g).to(torch.bfloat16) if resgate else None
     gate = torch.rand(N, generator=g).to(torch.bfloat16) if resgate else None
     _check(gpu, oracle_mod, qa, sa, fw, f"wide192 {M}x{N}x{K}", act=act, residual=res, gate=gate)
+
+
+@pytest.mark.parametrize("M,N,K,act,resgate", [(16, 1536, 6144, None, True), (1, 16, 256, "gelu_tanh", False),
+                                               (9, 48, 2048, None, True), (16, 2048, 1024, "gelu_tanh", True),
+                                               (13, 1024, 3072, None, False)])
+def test_skinny_row_halves(gpu, oracle_mod, M, N, K, act, resgate):
+    # one token block, unsplit K and <= 128 row groups: two workgroups per group,
+    # each streaming 8 of its 16 weight rows and storing their outputs; row-major
+    # and tile-layout weights, bit-identical, and repeated calls identical
+    from instinctflash_amd.kernels import fp8 as F, pack_skinny
+    qa, sa, fw, g = _make(gpu, M, N, K, seed=M * 3 + N + K, bias=True)
+    res = torch.randn((M, N), generator=g).to(torch.bfloat16) if resgate else None
+    gate = torch.rand(N, generator=g).to(torch.bfloat16) if resgate else None
+    o32, _ = _check(gpu, oracle_mod, qa, sa, fw, f"row halves {M}x{N}x{K}", act=act, residual=res, gate=gate)
+    kw = dict(act=act, residual=None if res is None else res.to(gpu), gate=None if gate is None else gate.to(gpu),
+              out_dtype=torch.float32)
+    got = F.linear(qa, sa, pack_skinny(fw), **kw)
+    assert torch.equal(got.view(torch.int32), o32.view(torch.int32)), f"tiled row halves {M}x{N}x{K}"
+    for _ in range(2):
+        assert torch.equal(F.linear(qa, sa, fw, **kw).view(torch.int32), o32.view(torch.int32))
