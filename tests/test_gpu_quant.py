@@ -219,6 +219,14 @@ def _deq(q, s):
     return q.float() * s[:, None]
 
 
+def _adjacent_codes(got, want):
+    """Every differing E4M3 code is one step from the recipe's (signed magnitude order)."""
+    a, b = got.astype(np.int32), want.astype(np.int32)
+    order = lambda c: np.where(c & 0x80, -(c & 0x7F), c & 0x7F)  # noqa: E731
+    d = a != b
+    return bool(np.all(np.abs(order(a) - order(b))[d] <= 1))
+
+
 def test_row_quant_gelu(gpu, oracle_mod):
     from instinctflash_amd.kernels import row_quant
     g = torch.Generator().manual_seed(22)
@@ -235,6 +243,7 @@ def test_row_quant_gelu(gpu, oracle_mod):
     # (tests/test_gi_kernels.py:127: |deq - h| / amax < 0.07).
     assert np.all(np.abs(_f(s).view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
     assert (_q(q) == eq).mean() > 0.999
+    assert _adjacent_codes(_q(q), eq)
     err = np.abs(_deq(q, s).cpu().numpy() - h) / np.abs(h).max(axis=1, keepdims=True)
     assert err.max() < 0.07
 
@@ -295,6 +304,7 @@ def test_gated_act_quant(gpu, oracle_mod, act):
     eq, es = oracle_mod.quant_rows(h.astype(np.float32))
     assert np.all(np.abs(_f(s).view(np.int32).astype(np.int64) - es.view(np.int32)) <= 8)
     assert (_q(q) == eq).mean() > 0.999
+    assert _adjacent_codes(_q(q), eq)
     err = np.abs(_deq(q, s).cpu().numpy() - h) / np.abs(h).max(axis=1, keepdims=True)
     assert err.max() < 0.07
 
