@@ -891,8 +891,12 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
 
   // Mode bits: 1 GELU-tanh (GeGLU for GLU), 2 SiLU (SwiGLU), 4 gate,
   // 8 residual, 16 runtime flags (f32 residual or output, any combination).
-  auto rows = [&](auto mode_tag) __attribute__((always_inline)) {
+  // NT (compile time): bf16 output rows stored nontemporally (e.nt_out); a
+  // runtime choice per store split every row into its own basic block and
+  // kept the rows' address arithmetic from being shared.
+  auto rows = [&](auto mode_tag, auto nt_tag) __attribute__((always_inline)) {
     constexpr int MD = decltype(mode_tag)::value;
+    constexpr bool NT = decltype(nt_tag)::value;
     constexpr bool kRt = (MD & 16) != 0;
     const int fl = e.flags;
     const bool act_gelu = kRt ? (fl & (GLU ? IFX_EPI_GEGLU : IFX_EPI_GELU_TANH)) != 0 : (MD & 1) != 0;
@@ -1010,7 +1014,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
                 o.x = pack_bf16x2(y[0], y[1]);
                 o.y = pack_bf16x2(y[2], y[3]);
                 uint16_t* op = orow + static_cast<int64_t>(t * kRowsPerPass) * e.ldo;
-                if (e.nt_out) st8_nt(op, o);
+                if constexpr (NT) st8_nt(op, o);
                 else *reinterpret_cast<uint2*>(op) = o;
               }
             }
@@ -1029,22 +1033,30 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   const bool plain_io = !(fl & (IFX_EPI_OUT_F32 | IFX_EPI_OUT_F16 | IFX_EPI_RES_F32));
   const int gr = ((fl & IFX_EPI_GATE) ? 4 : 0) | ((fl & IFX_EPI_RESIDUAL) ? 8 : 0);
   using std::integral_constant;
+  auto run = [&](auto md) __attribute__((always_inline)) {
+    if constexpr (decltype(md)::value == 16) {
+      rows(md, std::false_type{});
+    } else {
+      if (e.nt_out) rows(md, std::true_type{});
+      else rows(md, std::false_type{});
+    }
+  };
   if constexpr (GLU) {
     if (plain_io && gr == 0) {
-      if (fl & IFX_EPI_SWIGLU) rows(integral_constant<int, 2>{});
-      else rows(integral_constant<int, 1>{});
+      if (fl & IFX_EPI_SWIGLU) run(integral_constant<int, 2>{});
+      else run(integral_constant<int, 1>{});
     } else {
-      rows(integral_constant<int, 16>{});
+      run(integral_constant<int, 16>{});
     }
   } else {
     const bool gl = (fl & IFX_EPI_GELU_TANH) != 0;
-    if (!plain_io) rows(integral_constant<int, 16>{});
-    else if (gl && gr == 0) rows(integral_constant<int, 1>{});
-    else if (gl) rows(integral_constant<int, 16>{});
-    else if (gr == 0) rows(integral_constant<int, 0>{});
-    else if (gr == 8) rows(integral_constant<int, 8>{});
-    else if (gr == 12) rows(integral_constant<int, 12>{});
-    else rows(integral_constant<int, 16>{});
+    if (!plain_io) run(integral_constant<int, 16>{});
+    else if (gl && gr == 0) run(integral_constant<int, 1>{});
+    else if (gl) run(integral_constant<int, 16>{});
+    else if (gr == 0) run(integral_constant<int, 0>{});
+    else if (gr == 8) run(integral_constant<int, 8>{});
+    else if (gr == 12) run(integral_constant<int, 12>{});
+    else run(integral_constant<int, 16>{});
   }
 }
 
