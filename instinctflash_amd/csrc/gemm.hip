@@ -537,6 +537,33 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   const int kt0 = static_cast<int>(split * part.kstages);
   const int nk = static_cast<int>(min(static_cast<int64_t>(K / KB) - kt0, part.kstages));
 
+  // Epilogue operands of this lane (column scales, bias, adaLN gate) and this
+  // thread's token scale, loaded before the K loop so their latency hides
+  // under it (after the loop they were a serialized round trip per tile).
+  constexpr int kCols = GLU ? 16 * kFN : 32 * kFN;  // output columns of a wave tile
+  constexpr int kLanesPerRow = kCols / 4;
+  // whole rows per 64-lane pass, a power of two (12 lanes per row for 192-row
+  // GLU tiles: 4 rows, 16 lanes idle)
+  constexpr int kRowsPerPass = 64 / kLanesPerRow >= 8 ? 8 : 64 / kLanesPerRow >= 4 ? 4 : 64 / kLanesPerRow >= 2 ? 2 : 1;
+  constexpr int kRowIters = 32 / kRowsPerPass;
+  static_assert(32 % kRowsPerPass == 0, "epilogue row passes");
+  const int64_t nw = n0 + wn * (32 * kFN);                // first (packed) weight row of the wave tile
+  const int64_t mw = m0 + wm * kWT;                 // first token of the wave tile
+  const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
+  const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
+  const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
+  // lanes past kRowsPerPass whole rows (96-column tiles) have no column of their own
+  const bool col_ok = lane < kRowsPerPass * kLanesPerRow && c_out < (GLU ? e.N / 2 : e.N);
+  const int64_t np = col_ok ? nw + pc : 0;         // packed weight row (any valid row if unused)
+  const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
+  const float4 sw0 = epi_sw4(e, np);
+  const float4 b0 = load_f4_or(bp, np, 0.0f);
+  const float4 sw1 = GLU ? epi_sw4(e, np + 16) : sw0;
+  const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
+  uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
+  if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
+  const float sa_pre = tid < BM ? epi_sa(e, min(m0 + tid, e.M - 1)) : 0.0f;
+
   // DMA load i of a stage covers rows kRowsPerDma*blk .. +kRowsPerDma-1
   // (blk = wave*kLoads + i; weight rows first, then token rows). Rows past N/M
   // are clamped: computed, never stored. Addresses are formed per stage to keep
@@ -852,34 +879,13 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   // runtime-flag loop.
   // The barrier keeps the stage buffers alive until every wave is done with
   // its MFMAs and publishes the token scales.
-  constexpr int kCols = GLU ? 16 * kFN : 32 * kFN;  // output columns of a wave tile
-  constexpr int kLanesPerRow = kCols / 4;
-  // whole rows per 64-lane pass, a power of two (12 lanes per row for 192-row
-  // GLU tiles: 4 rows, 16 lanes idle)
-  constexpr int kRowsPerPass = 64 / kLanesPerRow >= 8 ? 8 : 64 / kLanesPerRow >= 4 ? 4 : 64 / kLanesPerRow >= 2 ? 2 : 1;
-  constexpr int kRowIters = 32 / kRowsPerPass;
-  static_assert(32 % kRowsPerPass == 0, "epilogue row passes");
-  const int64_t nw = n0 + wn * (32 * kFN);                // first (packed) weight row of the wave tile
-  const int64_t mw = m0 + wm * kWT;                 // first token of the wave tile
-  const int oc = (lane % kLanesPerRow) * 4;        // this lane's first output column in the tile
-  const int pc = GLU ? (oc / 16) * 32 + (oc % 16) : oc;  // its (gate) packed column
-  const int64_t c_out = (GLU ? nw / 2 : nw) + oc;
-  // lanes past kRowsPerPass whole rows (96-column tiles) have no column of their own
-  const bool col_ok = lane < kRowsPerPass * kLanesPerRow && c_out < (GLU ? e.N / 2 : e.N);
-  const int64_t np = col_ok ? nw + pc : 0;         // packed weight row (any valid row if unused)
-  const float* bp = (e.flags & IFX_EPI_BIAS) ? e.bias : nullptr;
-  const float4 sw0 = epi_sw4(e, np);
-  const float4 b0 = load_f4_or(bp, np, 0.0f);
-  const float4 sw1 = GLU ? epi_sw4(e, np + 16) : sw0;
-  const float4 b1 = GLU ? load_f4_or(bp, np + 16, 0.0f) : b0;
-  uint2 g2 = make_uint2(0x3F803F80u, 0x3F803F80u);  // bf16 1.0 x 4
-  if ((e.flags & IFX_EPI_GATE) && col_ok) g2 = *reinterpret_cast<const uint2*>(e.gate + c_out);
   if constexpr (kA3) {
     // s_sa overlays the ring: every wave must be done reading its last stage
     asm volatile("" ::: "memory");
     __syncthreads();
   }
-  for (int t = tid; t < BM; t += kWaves * 64) s_sa[t] = epi_sa(e, min(m0 + t, e.M - 1));
+  static_assert(kWaves * 64 >= BM, "one token scale per thread");
+  if (tid < BM) s_sa[tid] = sa_pre;
   asm volatile("" ::: "memory");
   __syncthreads();
   const float swa[4] = {sw0.x, sw0.y, sw0.z, sw0.w}, ba[4] = {b0.x, b0.y, b0.z, b0.w};
