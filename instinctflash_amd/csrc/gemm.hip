@@ -509,19 +509,21 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   static_assert(KB == 64 || KB == 128, "stage depth");
   constexpr int kPitch = 128 + 4;                  // floats per epilogue tile row
   constexpr int kEpiBytes = kWaves * 32 * kPitch * 4;
-  // The 4-wave wide tiles keep the token rows of three stages and the weight
-  // rows of two (a token-row ring one stage deeper than the weight-row ring):
-  // 2 x BN x 128 + 3 x 256 x 128 bytes (160 KB at BN = 256). The token scales
-  // of the epilogue then live in the ring's space after the K loop.
-  constexpr bool kA3 = FM == 4 && KB == 128 && STAGES == 2;
+  // The 4-wave wide tiles keep the weight rows of three stages and the token
+  // rows of two (a weight-row ring one stage deeper than the token-row ring):
+  // 3 x BN x 128 + 2 x 256 x 128 bytes (160 KB at BN = 256). In an engine the
+  // weights arrive from HBM while the token rows were just written by their
+  // producer (C5 step 1004 -> 996 us against the token rows three deep). The
+  // token scales of the epilogue then live in the ring's space after the K loop.
+  constexpr bool kW3 = FM == 4 && KB == 128 && STAGES == 2;
   constexpr int kWSlot = BN * KB, kASlot = BM * KB;  // bytes of one stage's weight / token rows
-  constexpr int kRing = kA3 ? 2 * kWSlot + 3 * kASlot : STAGES * kStage;
+  constexpr int kRing = kW3 ? 3 * kWSlot + 2 * kASlot : STAGES * kStage;
   constexpr int kSmem = kRing > kEpiBytes + BM * 4 ? kRing : kEpiBytes + BM * 4;
-  // the token scales (s_sa): after the ring, or (kA3) inside it after the K loop
-  constexpr int kLds = kA3 ? kSmem : kSmem + BM * 4;
+  // the token scales (s_sa): after the ring, or (kW3) inside it after the K loop
+  constexpr int kLds = kW3 ? kSmem : kSmem + BM * 4;
   static_assert(OCC * kLds <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
-  float* const s_sa = reinterpret_cast<float*>(smem + (kA3 ? kEpiBytes : kSmem));
+  float* const s_sa = reinterpret_cast<float*>(smem + (kW3 ? kEpiBytes : kSmem));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -646,17 +648,17 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     // < 4 GiB with rows and row strides below 2^24. DMA i of a stage covers
     // tile rows 8 * (wave * kLoads + i) + lrow (weight rows first).
     static_assert(kRowsPerDma == 8, "128-byte rows");
-    // Which 1 KB blocks (8 rows) of a stage wave `wave` fills: with kA3 every
+    // Which 1 KB blocks (8 rows) of a stage wave `wave` fills: with kW3 every
     // wave takes BN / 32 weight blocks and BM / 32 token blocks (the same
     // split for all waves, so all wait for the same counts); otherwise blocks
     // wave * kLoads .. + kLoads - 1 of [weight blocks | token blocks].
-    constexpr int kW4 = BN / 32, kA4 = BM / 32;  // kA3: weight / token DMAs per wave per stage
-    static_assert(!kA3 || kW4 + kA4 == kLoads, "kA3 DMA split");
-    const int iw = kA3 ? kW4 : BN / 8 - wave * kLoads;  // DMAs i < iw of this wave load weight rows
+    constexpr int kW4 = BN / 32, kA4 = BM / 32;  // kW3: weight / token DMAs per wave per stage
+    static_assert(!kW3 || kW4 + kA4 == kLoads, "kW3 DMA split");
+    const int iw = kW3 ? kW4 : BN / 8 - wave * kLoads;  // DMAs i < iw of this wave load weight rows
     uint32_t doff[kLoads];                  // per-lane byte offset of DMA i, stage kt0
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int blk = kA3 ? (i < kW4 ? wave * kW4 + i : BN / 8 + wave * kA4 + (i - kW4)) : wave * kLoads + i;
+      const int blk = kW3 ? (i < kW4 ? wave * kW4 + i : BN / 8 + wave * kA4 + (i - kW4)) : wave * kLoads + i;
       const int r = blk * 8 + lrow;
       const bool isw = i < iw;
       const uint32_t row = static_cast<uint32_t>(isw ? min(n0 + r, n_last) : min(m0 + (r - BN), m_last));
@@ -666,11 +668,14 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     const uint64_t wbase = reinterpret_cast<uintptr_t>(W), abase = reinterpret_cast<uintptr_t>(A);
     // LDS byte offsets (from smem) of stage kl's weight rows and token rows
     auto wslot = [&](int kl) -> uint32_t {
-      return kA3 ? (kl & 1) * kWSlot : (kl % STAGES) * kStage;
+      return kW3 ? (kl % 3) * kWSlot : (kl % STAGES) * kStage;
     };
     auto aslot = [&](int kl) -> uint32_t {
-      return kA3 ? 2 * kWSlot + (kl % 3) * kASlot : (kl % STAGES) * kStage + kWSlot;
+      return kW3 ? 3 * kWSlot + (kl & 1) * kASlot : (kl % STAGES) * kStage + kWSlot;
     };
+    // kW3: DMA index of issue slot m. The token rows are issued first and the
+    // weight rows after them, so the weight rows are the newest in flight.
+    auto dma_at = [](int m) { return kW3 ? (m < kA4 ? kW4 + m : m - kA4) : m; };
     // DMA i of this wave: weight rows of stage klw (i < iw) or token rows of
     // stage kla; block blk = wave * kLoads + i lands at row 8 * blk of its stage
     // (token rows counted from BN).
@@ -687,10 +692,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     // bases such that DMA i lands at base + i * 1024
     const uint32_t smem_off = lds_offset(smem);
     auto wdst_of = [&](int kl) {
-      return __builtin_amdgcn_readfirstlane(kA3 ? smem_off + wslot(kl) + wave * kW4 * 1024 : lds_base + wslot(kl));
+      return __builtin_amdgcn_readfirstlane(kW3 ? smem_off + wslot(kl) + wave * kW4 * 1024 : lds_base + wslot(kl));
     };
     auto adst_of = [&](int kl) {
-      return __builtin_amdgcn_readfirstlane(kA3 ? smem_off + aslot(kl) + (wave * kA4 - kW4) * 1024
+      return __builtin_amdgcn_readfirstlane(kW3 ? smem_off + aslot(kl) + (wave * kA4 - kW4) * 1024
                                                 : lds_base + aslot(kl) - kWSlot);
     };
     // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (2kFN+2j, 2kFN+2j+1)
@@ -723,26 +728,27 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     };
-    if constexpr (kA3) {
-      // Token rows three stages deep, weight rows two. Stage kt's second half
-      // issues the weight rows of stage kt+2 and the token rows of stage kt+3
-      // (weight DMAs first), both into the slots stage kt has just freed; the
-      // barrier of stage kt then needs everything but the newest token rows
-      // (stage kt+2), which stay in flight: token rows get two stages of lead.
-      // Prologue order per wave: W0 A0 W1 A1 A2 (each its own DMAs only).
+    if constexpr (kW3) {
+      // Weight rows three stages deep, token rows two. Stage kt's second half
+      // issues the token rows of stage kt+2 and the weight rows of stage kt+3
+      // (token DMAs first), both into the slots stage kt has just freed; the
+      // barrier of stage kt then needs everything but the newest weight rows
+      // (stage kt+2), which stay in flight: weight rows get two stages of lead.
+      // Prologue order per wave: A0 W0 A1 W1 W2 (each its own DMAs only).
 #pragma unroll
       for (int s = 0; s < 3; ++s) {
         const uint32_t wd = wdst_of(s), ad = adst_of(s);
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
+        for (int m = 0; m < kLoads; ++m) {
+          const int i = dma_at(m);
           if (i < iw) {
-            if (s < 2 && s < nk) dma_one(s, 0, wd, ad, i);
-          } else if (s < nk) {
+            if (s < nk) dma_one(s, 0, wd, ad, i);
+          } else if (s < 2 && s < nk) {
             dma_one(0, s, wd, ad, i);
           }
         }
       }
-      if (nk >= 3) wait_vmcnt<kW4 + 2 * kA4>();  // this wave's W1 A1 A2 may stay in flight
+      if (nk >= 3) wait_vmcnt<kLoads + kW4>();  // this wave's A1 W1 W2 may stay in flight
       else if (nk == 2) wait_vmcnt<kLoads>();
       else wait_vmcnt<0>();
     } else {
@@ -760,11 +766,11 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     sync();
 #pragma unroll
     for (int r = 0; r < kRd; ++r) read_one(smem + wslot(0), smem + aslot(0), fr[0], 0, r);  // stage 0's half 0
-    // kDmaW: stage kt + STAGES exists (its weight rows, or with kA3 its rows
-    // of both operands in the ring's form); kDmaA (kA3): stage kt + 3 exists.
-    auto stage = [&](int kt, auto dmaw_tag, auto dmaa_tag) {
-      constexpr bool kDmaW = decltype(dmaw_tag)::value;
-      constexpr bool kDmaA = decltype(dmaa_tag)::value;
+    // kDma2: stage kt + STAGES exists (kW3: its token rows are issued here);
+    // kDma3 (kW3): stage kt + 3 exists (its weight rows are issued here).
+    auto stage = [&](int kt, auto dma2_tag, auto dma3_tag) {
+      constexpr bool kDma2 = decltype(dma2_tag)::value;
+      constexpr bool kDma3 = decltype(dma3_tag)::value;
       const uint8_t* wcur = smem + wslot(kt);
       const uint8_t* acur = smem + aslot(kt);
       const uint8_t* wnxt = smem + wslot(kt + 1);  // after the last stage: a settled slot, unused
@@ -777,31 +783,32 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       }
       interleave();
       wait_lgkm0();
-      if constexpr (kA3) {
-        // stage kt+1 landed; the token rows of stage kt+2 may stay in flight
-        if (kt + 2 < nk) wait_vmcnt<kA4>();
+      if constexpr (kW3) {
+        // stage kt+1 landed; the weight rows of stage kt+2 may stay in flight
+        if (kt + 2 < nk) wait_vmcnt<kW4>();
         else if (kt + 1 < nk) wait_vmcnt<0>();
       } else {
-        if (kDmaW || kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();  // stages up to kt+STAGES-1 issued
+        if (kDma2 || kt + STAGES - 1 < nk) wait_vmcnt<(STAGES - 2) * kLoads>();  // stages up to kt+STAGES-1 issued
         else if (kt + 1 < nk) wait_vmcnt<0>();
       }
       sync();
-      // DMA destinations: kA3 weight rows of stage kt+2 and token rows of
-      // stage kt+3 (both the slots of stage kt); otherwise stage kt+STAGES
-      const uint32_t wd = wdst_of(kA3 ? kt + 2 : kt + STAGES);
-      const uint32_t ad = adst_of(kA3 ? kt + 3 : kt + STAGES);
+      // DMA destinations: kW3 weight rows of stage kt+3 and token rows of
+      // stage kt+2 (both the slots of stage kt); otherwise stage kt+STAGES
+      const uint32_t wd = wdst_of(kW3 ? kt + 3 : kt + STAGES);
+      const uint32_t ad = adst_of(kW3 ? kt + 2 : kt + STAGES);
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
         if (m < kMF) mfma_one(fr[1], m);
         read_one(wnxt, anxt, fr[0], 0, m);
         if (m < kLoads) {
-          if constexpr (kA3) {
-            if (m < iw) {
-              if constexpr (kDmaW) dma_one(kt + 2, 0, wd, ad, m);
+          if constexpr (kW3) {
+            const int i = dma_at(m);
+            if (i < iw) {
+              if constexpr (kDma3) dma_one(kt + 3, 0, wd, ad, i);
             } else {
-              if constexpr (kDmaA) dma_one(0, kt + 3, wd, ad, m);
+              if constexpr (kDma2) dma_one(0, kt + 2, wd, ad, i);
             }
-          } else if constexpr (kDmaW) {
+          } else if constexpr (kDma2) {
             dma_one(kt + STAGES, kt + STAGES, wd, ad, m);
           }
         }
@@ -811,7 +818,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     using std::false_type;
     using std::true_type;
     int kt = 0;
-    if constexpr (kA3) {
+    if constexpr (kW3) {
       for (; kt + 3 < nk; ++kt) stage(kt, true_type{}, true_type{});
       for (; kt + 2 < nk; ++kt) stage(kt, true_type{}, false_type{});
     } else {
@@ -879,7 +886,7 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
   // runtime-flag loop.
   // The barrier keeps the stage buffers alive until every wave is done with
   // its MFMAs and publishes the token scales.
-  if constexpr (kA3) {
+  if constexpr (kW3) {
     // s_sa overlays the ring: every wave must be done reading its last stage
     asm volatile("" ::: "memory");
     __syncthreads();
