@@ -700,28 +700,40 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     };
     // 16-byte fragment halves: W fragments i at (2i, 2i+1), token fragments j at (2kFN+2j, 2kFN+2j+1)
     v4i fr[2][kRd];
+    // Token fragments past M: a wave whose 32-token fragments j >= JV lie
+    // wholly past the last token (the last token tile of an M that is not a
+    // multiple of the tile) skips their LDS reads and MFMAs. JV is a
+    // compile-time count (kFM, kFM / 2 or 0), the smallest that covers the
+    // wave's tokens, so a partial tile costs fewer matrix-core cycles.
     // wp / ap: the stage's weight-row and token-row slots
-    auto read_one = [&](const uint8_t* wp, const uint8_t* ap, v4i* f, int h, int r) {
+    auto read_one = [&](const uint8_t* wp, const uint8_t* ap, v4i* f, int h, int r, auto jv_tag) {
+      constexpr int JV = decltype(jv_tag)::value;
       const int ch = 4 * h + 2 * fhalf + (r & 1);
       if (r < 2 * kFN) {
         f[r] = ld16(wp + S::off(wn * (32 * kFN) + (r >> 1) * 32 + frow, ch));
-      } else {
+      } else if ((r - 2 * kFN) >> 1 < JV) {
         f[r] = ld16(ap + S::off(wm * kWT + ((r - 2 * kFN) >> 1) * 32 + frow, ch));
       }
     };
 
-    auto mfma_one = [&](const v4i* f, int m) {
+    auto mfma_one = [&](const v4i* f, int m, auto jv_tag) {
+      constexpr int JV = decltype(jv_tag)::value;
       const int i = m / kFM, j = m % kFM;
-      acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[2 * kFN + 2 * j], f[2 * kFN + 2 * j + 1]), acc[i][j]);
+      if (j < JV)
+        acc[i][j] = mfma32(cat8(f[2 * i], f[2 * i + 1]), cat8(f[2 * kFN + 2 * j], f[2 * kFN + 2 * j + 1]), acc[i][j]);
     };
-    auto interleave = [] {  // keep the MFMA / LDS-read alternation
+    auto interleave = [](auto jv_tag) {  // keep the MFMA / LDS-read alternation
+      constexpr int JV = decltype(jv_tag)::value;
+      constexpr int kMFv = kFN * JV, kRdv = 2 * (kFN + JV);
 #pragma unroll
-      for (int m = 0; m < kMF; ++m) {
+      for (int m = 0; m < kMFv; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      if constexpr (kRd > kMF) __builtin_amdgcn_sched_group_barrier(0x100, kRd - kMF, 0);
+      if constexpr (kRdv > kMFv) __builtin_amdgcn_sched_group_barrier(0x100, kRdv - kMFv, 0);
     };
+    using std::integral_constant;
+    constexpr integral_constant<int, kFM> kAllFrags{};
     auto wait_lgkm0 = [] { __builtin_amdgcn_s_waitcnt(0xC07F); };  // lgkmcnt(0), visible to the compiler
     auto sync = [&] {
       asm volatile("" ::: "memory");
@@ -765,10 +777,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
     }
     sync();
 #pragma unroll
-    for (int r = 0; r < kRd; ++r) read_one(smem + wslot(0), smem + aslot(0), fr[0], 0, r);  // stage 0's half 0
+    for (int r = 0; r < kRd; ++r) read_one(smem + wslot(0), smem + aslot(0), fr[0], 0, r, kAllFrags);  // stage 0's half 0
     // kDma2: stage kt + STAGES exists (kW3: its token rows are issued here);
     // kDma3 (kW3): stage kt + 3 exists (its weight rows are issued here).
-    auto stage = [&](int kt, auto dma2_tag, auto dma3_tag) {
+    auto stage = [&](int kt, auto dma2_tag, auto dma3_tag, auto jv) {
       constexpr bool kDma2 = decltype(dma2_tag)::value;
       constexpr bool kDma3 = decltype(dma3_tag)::value;
       const uint8_t* wcur = smem + wslot(kt);
@@ -778,10 +790,10 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       wait_lgkm0();
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
-        if (m < kMF) mfma_one(fr[0], m);
-        read_one(wcur, acur, fr[1], 1, m);
+        if (m < kMF) mfma_one(fr[0], m, jv);
+        read_one(wcur, acur, fr[1], 1, m, jv);
       }
-      interleave();
+      interleave(jv);
       wait_lgkm0();
       if constexpr (kW3) {
         // stage kt+1 landed; the weight rows of stage kt+2 may stay in flight
@@ -798,8 +810,8 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
       const uint32_t ad = adst_of(kW3 ? kt + 2 : kt + STAGES);
 #pragma unroll
       for (int m = 0; m < kRd; ++m) {
-        if (m < kMF) mfma_one(fr[1], m);
-        read_one(wnxt, anxt, fr[0], 0, m);
+        if (m < kMF) mfma_one(fr[1], m, jv);
+        read_one(wnxt, anxt, fr[0], 0, m, jv);
         if (m < kLoads) {
           if constexpr (kW3) {
             const int i = dma_at(m);
@@ -813,18 +825,25 @@ __global__ __launch_bounds__(4 * BM / FM, OCC) void gemm_big(const uint8_t* __re
           }
         }
       }
-      interleave();
+      interleave(jv);
     };
     using std::false_type;
     using std::true_type;
-    int kt = 0;
-    if constexpr (kW3) {
-      for (; kt + 3 < nk; ++kt) stage(kt, true_type{}, true_type{});
-      for (; kt + 2 < nk; ++kt) stage(kt, true_type{}, false_type{});
-    } else {
-      for (; kt + STAGES < nk; ++kt) stage(kt, true_type{}, false_type{});
-    }
-    for (; kt < nk; ++kt) stage(kt, false_type{}, false_type{});
+    auto kloop = [&](auto jv) {
+      int kt = 0;
+      if constexpr (kW3) {
+        for (; kt + 3 < nk; ++kt) stage(kt, true_type{}, true_type{}, jv);
+        for (; kt + 2 < nk; ++kt) stage(kt, true_type{}, false_type{}, jv);
+      } else {
+        for (; kt + STAGES < nk; ++kt) stage(kt, true_type{}, false_type{}, jv);
+      }
+      for (; kt < nk; ++kt) stage(kt, false_type{}, false_type{}, jv);
+    };
+    // wave-uniform: 32-token fragments of this wave that hold a token < M
+    const int64_t jv = (e.M - mw + 31) / 32;
+    if (jv > kFM / 2) kloop(kAllFrags);
+    else if (jv > 0) kloop(integral_constant<int, kFM / 2>{});
+    else kloop(integral_constant<int, 0>{});
     wait_vmcnt<0>();  // no DMA may still write LDS when the epilogue reuses it
   } else {
 #pragma unroll
