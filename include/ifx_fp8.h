@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define IFX_ABI_VERSION 2
+#define IFX_ABI_VERSION 3
 
 /* status codes (negative = rejected before launch) */
 #define IFX_OK 0
@@ -187,11 +187,10 @@ int ifx_dequant_rows(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t
  * lda/ldw multiples of 16, ldo/ldr multiples of 8. sa: f32 [M] or NULL,
  * sw: f32 [N] or NULL, bias: f32 [N] or NULL, gate: bf16 [N_out] or NULL.
  * workspace: at least ifx_fp8_linear_workspace_size(M,N,K,epilogue) bytes of
- * 16-byte aligned device memory, used when the GEMM splits K across
- * workgroups (too few output tiles, or for M <= 64 too few 16-row groups and a
- * long K, to fill the GPU); the size is 0 (NULL allowed) otherwise. Layout: a 1 KB header
- * of per-group arrival counters, then fp32 partial sums. Zero-fill a workspace
- * once before its first use; every call leaves the header zeroed again, so one
+ * 16-byte aligned device memory, used when the GEMM (M > 64) splits K across
+ * workgroups because it has too few output tiles to fill the GPU: the slices'
+ * fp32 partial sums, added by a second launch. The size is 0 (NULL allowed)
+ * otherwise, and always for M <= 64. No initialisation is needed; one
  * workspace serves any sequence of calls and shapes. Calls that may overlap
  * must not share a workspace.
  * With sa = sw = NULL and epilogue 0 this is the raw-accumulator GEMM of
@@ -285,7 +284,7 @@ int ifx_qkv_split(const void* qkv, int qkv_dtype, int64_t ldqkv, const float* ro
  * (IFX_EPI_W_TILED, ifx_fp8_pack_skinny). flags: IFX_EPI_BIAS, IFX_EPI_W_TILED,
  * IFX_EPI_A_TILED only. head_dim % 16 == 0, <= 256; inv_freq NULL = no rotation;
  * kv_base_dev: NULL or a device int32 read in place of kv_base; out_dtype BF16, F16
- * or F32. Workspace as ifx_fp8_linear(M, N, K, 0).
+ * or F32. workspace / ws_bytes: unused (M <= 64 needs none); NULL / 0 allowed.
  * Replaces: the pair ifx_fp8_linear (raw accumulator, reference
  * instinctflash/kernels/fp8.py:50-53 `gemm`) + ifx_qkv_split (reference
  * instinctflash/kernels/rope.py:89-116) at decode / action-chunk sizes; the
@@ -329,9 +328,8 @@ int ifx_wan_qkv(const void* raw, int raw_dtype, int64_t ldraw, const float* row,
  * ifx_fp8_linear on the result with the same weight / epilogue arguments: two
  * launches, the output bit-identical to those two calls in sequence.
  * IFX_SCALE_TENSOR needs ldx == K (else IFX_ERR_UNSUPPORTED).
- * workspace: ifx_quant_linear_workspace_size(...) bytes, 256-byte aligned,
- * zero-filled once before first use like ifx_fp8_linear's (its header comes
- * first); calls that may overlap must not share one.
+ * workspace: ifx_quant_linear_workspace_size(...) bytes, 256-byte aligned, no
+ * initialisation needed; calls that may overlap must not share one.
  * a_scale: NULL, or [M] f32 (IFX_SCALE_ROW) / [1] f32 (IFX_SCALE_TENSOR) that
  * receives the activation scales. IFX_EPI_SCALAR_SA is rejected (the scale is
  * computed here); IFX_EPI_SCALAR_SW is honoured.
@@ -414,8 +412,7 @@ int ifx_attention(const void* q, const void* k, const void* v, void* o, int dtyp
                   size_t ws_bytes, void* q8, int64_t ldq8, float* q8_scale, void* stream);
 
 /*
- * ifx_quant_linear without a workspace argument: the same two launches (plus a
- * one-workgroup clear of the split-K ticket header), bit-identical output, but
+ * ifx_quant_linear without a workspace argument: the same launches, bit-identical output, but
  * the workspace is a fixed scratch array inside the library
  * (ifx_quant_linear_noalloc_max_bytes() = 64 MiB per GPU, held from the first
  * call on that GPU until the process ends). No allocation of any kind.

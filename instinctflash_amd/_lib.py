@@ -13,7 +13,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = Path(os.environ.get("IFX_FP8_LIBRARY", Path(__file__).resolve().parent / "libifx_fp8.so"))
 
 # Status codes (include/ifx_fp8.h)

@@ -1136,24 +1136,22 @@ __global__ __launch_bounds__(256) void splitk_reduce(Partials part, int ksplit, 
 // Skinny kernel (M <= 64): weight streaming
 // ---------------------------------------------------------------------------
 //
-// A group of 16 weight rows (32 for GLU: a gate block and its up block) is
-// split along K into ksplit slices, one workgroup per (group, slice), so that
-// shapes with few row groups still spread their bytes over every CU (a CU's
-// memory concurrency, not HBM, bounds a skinny GEMM that leaves CUs idle).
-// Inside a workgroup the WAVES waves split the slice's K steps (wave w takes
-// steps w, w+WAVES, ...), each loading kSkUnroll steps of weight fragments
-// (nontemporal: read once per call) and token fragments before issuing their
-// MFMAs; partial sums are added in LDS in wave order.
-//
-// With ksplit > 1 each workgroup stores its fp32 partial and takes a ticket
-// on its group's counter (an agent-scope release, so the partial is visible
-// device-wide first); the workgroup that takes the last ticket adds the
-// slices' partials in slice order (deterministic), resets the counter to zero
-// and runs the epilogue. No workgroup waits for another.
+// A workgroup owns a group of 16 weight rows (32 for GLU: a gate block and
+// its up block) and the whole of K. Inside it the WAVES waves split the K
+// steps (wave w takes steps w, w+WAVES, ...), each loading kSkUnroll steps of
+// weight fragments (nontemporal: read once per call) and token fragments
+// before issuing their MFMAs; partial sums are added in LDS in wave order.
+// Shapes with few row groups spread over more CUs by token blocks (tsplit) or
+// row halves (rhalves), never by splitting K: a K split needs a device-wide
+// handoff of partial sums between workgroups, and its agent-scope
+// release/acquire (a write-back and an invalidation of the XCD's L2) costs
+// more than the split wins. Measured on MI355X with weights streamed from HBM,
+// two K slices with an acquire-release ticket against one workgroup per group:
+// 16x512x8192 8.9 / 7.6 us, 1x1024x16384 16.7 / 9.7, 8x2048x8192 19.4 / 7.8,
+// 16x1536x6144 15.2 / 7.1; three and four slices lose more.
 
 constexpr int kSkUnroll = 4;       // K steps whose loads are issued together per wave
-constexpr int kSkMaxGroups = 256;  // row groups that may split K (one ticket each)
-constexpr size_t kWsHeader = kSkMaxGroups * sizeof(int);  // tickets at the workspace start
+constexpr int kSkMaxGroups = 256;  // row groups up to which a group may take two workgroups (row halves)
 
 // The qkv_split epilogue of ifx_fp8_linear_qkv_rope (flag kEpiRopeQkv): the
 // fused q|k|v weight rows are permuted per head so that packed rows
@@ -1218,11 +1216,7 @@ __device__ __forceinline__ void rope_qkv_store(const RopeQkv& r, int64_t m, int6
   store_elem(r.out_dtype, dst, off + half + d + 1, hi1);
 }
 
-struct SkSplit {
-  float* part;     // [ksplit][groups][NBW][MB][64 lanes] x 4 floats
-  int* tickets;    // [groups], zero between calls
-  int ksplit;
-  int64_t kss;     // K steps per slice
+struct SkArgs {
   RopeQkv rope;    // the qkv_split epilogue's arguments (flag kEpiRopeQkv)
 };
 
@@ -1230,12 +1224,9 @@ struct SkinnyPlan {
   int mb;          // 16-token blocks per workgroup (1..4)
   int nbw;         // 16-row weight blocks per workgroup (1, or 2 for GLU)
   int64_t groups;  // row groups
-  int ksplit;      // K slices per group (one workgroup each)
-  int64_t kss;     // K steps per slice
   int waves;       // waves per workgroup (4, 8 or 16)
   int tsplit;      // workgroups along the tokens per group (each owns mb blocks)
   int rhalves;     // workgroups along the group's 16 weight rows (2: 8 rows each)
-  size_t ws_bytes; // workspace (tickets + partials) when ksplit > 1
 };
 
 __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu) {
@@ -1244,17 +1235,6 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   p.nbw = glu ? 2 : 1;
   p.groups = N / (16 * p.nbw);
   const int64_t ksteps = (K + kBK - 1) / kBK;
-  // Split K in two for one token block, at most 128 row groups and a long K
-  // (>= 64 steps of 128): the two halves' chains run side by side. Measured
-  // on MI355X with weights streamed from HBM (tile layouts), split / not:
-  // 16x512x8192 6.3 / 6.9 us, 8x2048x8192 7.4 / 8.3, 1x1024x16384 9.2 / 11.3;
-  // at K = 3072..6144 the ticket and partial round trip costs more than it
-  // wins (16x1536x6144 6.3 / 6.2, 16x1024x4096 5.5 / 4.8). More slices, or
-  // any split with several token blocks, lose more.
-  int64_t s = 1;
-  if (p.mb == 1 && p.groups <= kSkMaxGroups / 2 && ksteps >= 64) s = 2;
-  p.kss = (ksteps + s - 1) / s;
-  p.ksplit = static_cast<int>((ksteps + p.kss - 1) / p.kss);
   // One token block per workgroup (grid.y over the blocks) when the row groups
   // alone leave CUs idle: the extra reads of each weight fragment hit L2, and
   // each workgroup's MFMA and load chain gets 1/mb as long. Measured (M = 50,
@@ -1263,33 +1243,30 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
   // break even (50x8192x1024 GeGLU 7.6 -> 9.1 us; 50x4096x1024 with its
   // weights L2/MALL-resident 4.7 -> 4.9 us, streamed from HBM 6.5 -> 5.6 us).
   p.tsplit = 1;
-  if (p.ksplit == 1 && p.mb > 1 && p.nbw == 1 && p.groups < 256) {
+  if (p.mb > 1 && p.nbw == 1 && p.groups < 256) {
     p.tsplit = p.mb;
     p.mb = 1;
   }
   // GLU weights with four token blocks: two workgroups of two blocks each
   // (50x8192x1024 GeGLU 7.5 -> 6.5 us; one block each is slower, and so is
   // splitting two blocks: 32x8192x2048 SwiGLU 7.5 -> 7.7 us).
-  if (p.ksplit == 1 && p.nbw == 2 && p.mb == 4 && p.groups <= 256) {
+  if (p.nbw == 2 && p.mb == 4 && p.groups <= 256) {
     p.tsplit = 2;
     p.mb = 2;
   }
-  // Too few row groups to reach every CU (one 16-token block, unsplit K): two
+  // Too few row groups to reach every CU (one 16-token block): two
   // workgroups per group, each streaming 8 of its 16 weight rows (the other 8
   // MFMA rows are zeros and their outputs are not stored). The matrix cores
   // are idle here anyway; the weight stream spreads over twice the CUs.
   p.rhalves = 1;
-  if (p.ksplit == 1 && p.mb == 1 && p.tsplit == 1 && p.nbw == 1 && p.groups * 2 <= kSkMaxGroups) p.rhalves = 2;
-  // Enough waves that every wave has at most kSkUnroll K steps of its slice
+  if (p.mb == 1 && p.tsplit == 1 && p.nbw == 1 && p.groups * 2 <= kSkMaxGroups) p.rhalves = 2;
+  // Enough waves that every wave has at most kSkUnroll K steps
   // (one batch of loads in flight); 16 waves leave 128 VGPRs each, enough
   // for one 16 x 16 block only.
   int w = 4;
   const int wmax = p.nbw * p.mb == 1 ? 16 : 8;
-  while (w < wmax && p.kss > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
+  while (w < wmax && ksteps > static_cast<int64_t>(w) * kSkUnroll && 2 * w * p.nbw * p.mb <= 32) w *= 2;
   p.waves = w;
-  p.ws_bytes = p.ksplit > 1
-                   ? kWsHeader + static_cast<size_t>(p.ksplit) * p.groups * p.nbw * p.mb * 64 * 4 * sizeof(float)
-                   : 0;
   return p;
 }
 
@@ -1299,9 +1276,8 @@ __host__ inline SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, bool glu
 template <int MB, int NBW, int WAVES, bool TILED, int RH = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restrict__ A, int64_t lda,
                                                           const uint8_t* __restrict__ W, int64_t ldw,
-                                                          int64_t K, Epi e, SkSplit sp) {
+                                                          int64_t K, Epi e, SkArgs sp) {
   __shared__ v4f red[WAVES][NBW][MB][64];
-  __shared__ int is_last;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -1309,8 +1285,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   // RH > 1: RH workgroups split the group's 16 weight rows (16 / RH each)
   const int rh = RH == 1 ? 0 : static_cast<int>(blockIdx.x % RH);
   const int64_t bx = static_cast<int64_t>(blockIdx.x) / RH;
-  const int64_t grp = bx % groups;
-  const int slice = static_cast<int>(bx / groups);
+  const int64_t grp = bx;
   const int64_t nrow0 = grp * (16 * NBW);
   const int frow = lane & 15;
   const int g = lane >> 4;
@@ -1318,8 +1293,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const bool wmine = RH == 1 || frow / (16 / RH) == rh;
   const bool omine = RH == 1 || (4 * g) / (16 / RH) == rh;
   const int64_t ksteps = (K + kBK - 1) / kBK;
-  const int64_t s_begin = slice * sp.kss;
-  const int64_t s_end = min(s_begin + sp.kss, ksteps);
+  const int64_t s_end = ksteps;
   const bool a_tiled = (e.flags & IFX_EPI_A_TILED) != 0;  // A in the skinny tile layout (lda unused)
   const int64_t mb0 = static_cast<int64_t>(blockIdx.y) * MB;  // first 16-token block of this workgroup
 
@@ -1367,7 +1341,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[b][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t s0 = s_begin + wave; s0 < s_end; s0 += WAVES * kSkUnroll) {
+  for (int64_t s0 = wave; s0 < s_end; s0 += WAVES * kSkUnroll) {
     v8i wf[kSkUnroll][NBW];
     v8i af[kSkUnroll][MB];
 #pragma unroll
@@ -1422,40 +1396,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
       sum[b] = red[0][b][j][lane];
 #pragma unroll
       for (int w = 1; w < WAVES; ++w) sum[b] += red[w][b][j][lane];
-    }
-  }
-
-  if (sp.ksplit > 1) {
-    // Publish this slice's partial; the last workgroup of the group adds them.
-    auto part = [&](int sl, int b) {
-      return sp.part + ((((static_cast<int64_t>(sl) * groups + grp) * NBW + b) * MB + j) * 64 + lane) * 4;
-    };
-    // Ordering (HIP memory model): every wave's partial stores precede the
-    // barrier; thread 0's ticket is an agent-scope acquire-release RMW, so its
-    // release makes all of them (cumulatively, through the barrier) visible
-    // device-wide before the count moves. The last arriver's RMW acquires every
-    // earlier slice's release; the barrier and each wave's agent-scope acquire
-    // fence extend that to all of its waves before they read the partials.
-    if (wave < MB) {
-#pragma unroll
-      for (int b = 0; b < NBW; ++b) *reinterpret_cast<v4f*>(part(slice, b)) = sum[b];
-    }
-    __syncthreads();
-    if (tid == 0) {
-      const int t = __hip_atomic_fetch_add(sp.tickets + grp, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      is_last = t == sp.ksplit - 1;
-      // reset for the next call (ordered after this kernel by the stream)
-      if (is_last) __hip_atomic_store(sp.tickets + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (wave < MB) {
-#pragma unroll
-      for (int b = 0; b < NBW; ++b) {
-        sum[b] = *reinterpret_cast<const v4f*>(part(0, b));
-        for (int sl = 1; sl < sp.ksplit; ++sl) sum[b] += *reinterpret_cast<const v4f*>(part(sl, b));
-      }
     }
   }
 
@@ -1528,7 +1468,7 @@ __host__ inline BigPlan big_plan(int64_t M, int64_t N, int64_t K, int bm, int bn
   }
   p.kstages = (nk + s - 1) / s;
   p.ksplit = static_cast<int>((nk + p.kstages - 1) / p.kstages);
-  p.ws_bytes = p.ksplit > 1 ? kWsHeader + static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
+  p.ws_bytes = p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
   return p;
 }
 
@@ -1540,7 +1480,7 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
   Partials part{nullptr, e.N, p.kstages};
   if (p.ksplit > 1) {
     if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
-    part.base = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);  // tickets stay untouched
+    part.base = static_cast<float*>(ws);
   }
   const TileMap t = make_tile_map(p.tiles_m, p.tiles_n, p.ksplit);
   hipLaunchKernelGGL((gemm_big<BM, BN, KB, STAGES, OCC, GLU, FM>), dim3(static_cast<unsigned>(8 * t.per_xcd)), dim3(4 * BM / FM),
@@ -1555,8 +1495,8 @@ int launch_big(const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int
 
 template <int MB, int NBW, int WAVES>
 void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                     const Epi& e, const SkSplit& sp, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(p.groups * p.ksplit * p.rhalves), static_cast<unsigned>(p.tsplit)),
+                     const Epi& e, const SkArgs& sp, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(p.groups * p.rhalves), static_cast<unsigned>(p.tsplit)),
       block(WAVES * 64);
   if constexpr (MB == 1 && NBW == 1) {
     if (p.rhalves == 2) {
@@ -1575,7 +1515,7 @@ void launch_skinny_w(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const u
 
 template <int MB, int NBW>
 void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                      const Epi& e, const SkSplit& sp, hipStream_t st) {
+                      const Epi& e, const SkArgs& sp, hipStream_t st) {
   // 16 waves (128 VGPRs each) only for one 16 x 16 output block per workgroup:
   // more blocks' fragments do not fit without spilling
   if constexpr (NBW * MB == 1) {
@@ -1595,13 +1535,8 @@ void launch_skinny_mb(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const 
 
 template <int NBW>
 int launch_skinny(const SkinnyPlan& p, const uint8_t* a, int64_t lda, const uint8_t* w, int64_t ldw, int64_t K,
-                  const Epi& e, void* ws, size_t ws_bytes, hipStream_t st, const RopeQkv* rope = nullptr) {
-  SkSplit sp{nullptr, nullptr, p.ksplit, p.kss, rope ? *rope : RopeQkv{}};
-  if (p.ksplit > 1) {
-    if (!ws || ws_bytes < p.ws_bytes || !aligned16(ws)) return IFX_ERR_WORKSPACE;
-    sp.tickets = static_cast<int*>(ws);
-    sp.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kWsHeader);
-  }
+                  const Epi& e, hipStream_t st, const RopeQkv* rope = nullptr) {
+  const SkArgs sp{rope ? *rope : RopeQkv{}};
   switch (p.mb) {
     case 1: launch_skinny_mb<1, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
     case 2: launch_skinny_mb<2, NBW>(p, a, lda, w, ldw, K, e, sp, st); break;
@@ -1738,7 +1673,7 @@ extern "C" {
 
 size_t ifx_fp8_linear_workspace_size(int64_t M, int64_t N, int64_t K, int epilogue) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  if (M <= kSkinnyMaxM) return skinny_plan(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0).ws_bytes;
+  if (M <= kSkinnyMaxM) return 0;  // the skinny kernel needs no workspace
   if (!big_path(M, K)) return 0;
   switch (pick_big(M, N, K, (epilogue & (IFX_EPI_GEGLU | IFX_EPI_SWIGLU)) != 0)) {
     case BigCfg::kWide192: return big_plan(M, N, K, 256, 192, 128).ws_bytes;
@@ -1794,16 +1729,16 @@ constexpr int64_t kNtOutBytes = int64_t(32) << 20;
 
 inline size_t round256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
-// Workspace of ifx_quant_linear: the GEMM's own workspace first (its ticket
-// header must sit at offset 0 of every workspace), then the e4m3 copy of x
-// (row stride K), the per-token scales and the per-tensor amax partials.
+// Workspace of ifx_quant_linear: the GEMM's own workspace first (split-K
+// partials), then the e4m3 copy of x (row stride K), the per-token scales and
+// the per-tensor amax partials.
 struct QlWorkspace {
   size_t gemm, q, scale, partial, total;
 };
 
 QlWorkspace ql_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int scale_mode) {
   QlWorkspace w{};
-  w.gemm = round256(std::max(ifx_fp8_linear_workspace_size(M, N, K, epilogue), kWsHeader));
+  w.gemm = round256(ifx_fp8_linear_workspace_size(M, N, K, epilogue));
   w.q = round256(static_cast<size_t>(M) * K);
   w.scale = round256(static_cast<size_t>(M) * sizeof(float));
   w.partial = scale_mode == IFX_SCALE_TENSOR ? round256(ifx_quant_tensor_workspace_size(M * K)) : 0;
@@ -1835,8 +1770,7 @@ int ifx_fp8_linear(const void* a, int64_t lda, const float* sa, const void* w, i
 
   if (M <= kSkinnyMaxM) {
     const SkinnyPlan p = skinny_plan(M, N, K, glu);
-    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st)
-               : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, workspace, ws_bytes, st);
+    return glu ? launch_skinny<2>(p, A, lda, Wt, ldw, K, e, st) : launch_skinny<1>(p, A, lda, Wt, ldw, K, e, st);
   }
   if (big_path(M, K)) {
     const int64_t out_bytes = M * (glu ? N / 2 : N) * static_cast<int64_t>(sizeof(uint16_t));
@@ -1861,6 +1795,8 @@ int ifx_fp8_linear_qkv_rope(const void* a, int64_t lda, const float* sa, const v
                             const int32_t* kv_base_dev, int64_t M, int64_t K, void* workspace, size_t ws_bytes,
                             void* stream) {
   constexpr int kAllowed = IFX_EPI_BIAS | IFX_EPI_W_TILED | IFX_EPI_A_TILED;
+  (void)workspace;  // the skinny kernel needs none (ifx_fp8_linear_workspace_size is 0 for M <= 64)
+  (void)ws_bytes;
   if (flags & ~kAllowed) return IFX_ERR_INVALID;
   if (out_dtype != IFX_DTYPE_BF16 && out_dtype != IFX_DTYPE_F16 && out_dtype != IFX_DTYPE_F32) return IFX_ERR_INVALID;
   if (heads_q <= 0 || heads_kv <= 0 || head_dim <= 0 || head_dim % 16 != 0 || kv_base < 0) return IFX_ERR_INVALID;
@@ -1884,7 +1820,7 @@ int ifx_fp8_linear_qkv_rope(const void* a, int64_t lda, const float* sa, const v
                   v_out, sv_t, sv_h, kv_base, kv_base_dev, out_dtype};
   const SkinnyPlan p = skinny_plan(M, N, K, false);
   return launch_skinny<1>(p, static_cast<const uint8_t*>(a), lda, static_cast<const uint8_t*>(w), ldw, K, e,
-                          workspace, ws_bytes, static_cast<hipStream_t>(stream), &r);
+                          static_cast<hipStream_t>(stream), &r);
 }
 
 size_t ifx_fp8_skinny_tiled_bytes(int64_t N, int64_t K) {
@@ -1967,7 +1903,7 @@ int ifx_quant_linear(const void* x, int64_t ldx, int scale_mode, const void* w, 
 //
 // For callers that cannot allocate (code under HIP graph capture, serving
 // loops that forbid hipMalloc). The workspace of ifx_quant_linear (split-K
-// tickets and partials, the e4m3 copy of x, the scales) lives in `scratch`, a
+// partials, the e4m3 copy of x, the scales) lives in `scratch`, a
 // file-scope device array: every GPU the library runs on holds its own copy
 // (at its own address) until the process ends. Host code never passes the
 // array's name to a kernel (in host code it names a host-side shadow); it uses
@@ -2009,13 +1945,6 @@ void* scratch_ptr(int* rc) {
   return g_scratch[dev];
 }
 
-// Zeroes n 32-bit words (the split-K ticket header); a kernel rather than
-// hipMemsetAsync so the call stays graph-capturable without memset nodes.
-__global__ __launch_bounds__(256) void zero_words(int* p, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
 }  // namespace
 
 extern "C" {
@@ -2027,19 +1956,13 @@ int ifx_quant_linear_noalloc(const void* x, int64_t ldx, int scale_mode, const v
                              const void* gate, int epilogue, void* out, int64_t ldo, int64_t M, int64_t N,
                              int64_t K, float* a_scale, void* stream) {
   if (M < 0 || N <= 0 || K <= 0) return IFX_ERR_INVALID;
-  // every contract check before the clear below: a rejected call launches nothing
+  // every contract check before the scratch is touched: a rejected call launches nothing
   int rc = check_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K);
   if (rc != IFX_OK || M == 0) return rc;
   const size_t need = ql_workspace(M, N, K, epilogue, scale_mode).total;
   if (need > kScratchBytes) return IFX_ERR_SCRATCH;
   void* ws = scratch_ptr(&rc);
   if (!ws) return rc;
-  // The ticket header must read zero. Every call leaves it so, but a call that
-  // was rejected or interrupted mid-way need not have; clear it each time.
-  hipLaunchKernelGGL(zero_words, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<int*>(ws),
-                     static_cast<int>(kWsHeader / sizeof(int)));
-  rc = launch_status();
-  if (rc != IFX_OK) return rc;
   return ifx_quant_linear(x, ldx, scale_mode, w, ldw, sw, bias, residual, ldr, gate, epilogue, out, ldo, M, N, K,
                           a_scale, ws, kScratchBytes, stream);
 }

@@ -137,8 +137,8 @@ _RETIRED: list = []
 
 def _workspace(nbytes: int, device, stream: int):
     """Workspace per (device, stream), reused by every call on that stream
-    (calls on one stream are ordered). Zero-filled when allocated: its header
-    holds the split-K arrival counters, which every call leaves at zero.
+    (calls on one stream are ordered). It holds split-K partial sums, which
+    every call writes before it reads them, so it needs no initialisation.
 
     A buffer outgrown by a later call is kept alive (never freed), because a
     captured HIP graph may still hold its address. Growing while the stream is
@@ -154,7 +154,7 @@ def _workspace(nbytes: int, device, stream: int):
                                "capture; run the captured calls once before capturing")
         if ws is not None:
             _RETIRED.append(ws)
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

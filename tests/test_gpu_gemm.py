@@ -306,8 +306,8 @@ def test_contract_errors(gpu):
 
 
 def test_workspace_reuse_across_shapes(gpu, oracle_mod):
-    # Regression: split-K calls with different plans share one workspace per
-    # stream; a call must never read another call's partials as its tickets.
+    # Regression: calls with different plans share one workspace per stream,
+    # whatever an earlier call left in it.
     seq = [(16, 64, 4096), (16, 1536, 6144), (64, 256, 2048), (1, 512, 8192), (16, 1536, 6144), (50, 96, 4096)]
     for i, (M, N, K) in enumerate(seq):
         qa, sa, fw, _ = _make(gpu, M, N, K, seed=100 + i)
@@ -326,18 +326,18 @@ def test_split_k_shapes(gpu, oracle_mod, M, N, K, act):
     from instinctflash_amd import _lib
     from instinctflash_amd.kernels import fp8 as F, pack_glu
     glu = act in ("geglu", "swiglu")
-    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) > 1024
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) > 0
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N, bias=True)
     res = torch.randn((M, N // 2 if glu else N), generator=g).to(torch.bfloat16)
     w = pack_glu(fw) if glu else fw
     o32, o16 = _check(gpu, oracle_mod, qa, sa, w, f"split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
-    # repeated calls: bit-identical (fixed slice order) and the counters return to zero
+    # repeated calls: bit-identical (fixed slice order), the workspace
+    # overwritten with a nonzero pattern in between
     for _ in range(3):
+        for ws in F._WORKSPACES.values():
+            ws.fill_(0xA5)
         again = F.linear(qa, sa, w, act=act, residual=res.to(gpu), out_dtype=torch.float32)
         assert torch.equal(again.view(torch.int32), o32.view(torch.int32))
-    torch.cuda.synchronize()
-    for ws in F._WORKSPACES.values():
-        assert int(ws[:1024].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
     # in place: out aliases the residual
     r = res.to(gpu).clone()
     F.linear(qa, sa, w, out=r, act=act, residual=r)
@@ -419,9 +419,10 @@ def test_skinny_token_block_forms(gpu, oracle_mod, M, N, K, act):
     assert torch.equal(got.view(torch.int32), o32.view(torch.int32)), f"tiled skinny blocks {M}x{N}x{K}"
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096)])
-def test_skinny_shorter_k_is_not_split(gpu, M, N, K):
-    # K < 64 steps: one workgroup per row group (the split's round trip costs more)
+@pytest.mark.parametrize("M,N,K", [(16, 1536, 6144), (16, 768, 3072), (8, 1024, 4096), (1, 1024, 16384),
+                                   (16, 512, 8192)])
+def test_skinny_needs_no_workspace(gpu, M, N, K):
+    # M <= 64 never splits K across workgroups
     from instinctflash_amd import _lib
     assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, 0) == 0
 
@@ -473,26 +474,25 @@ def test_fp8_linear_module(gpu, oracle_mod):
 
 @pytest.mark.parametrize("M,N,K,act", [(16, 1536, 8192, None), (1, 512, 8208, None), (9, 1024, 8336, "gelu_tanh"),
                                        (16, 2048, 8192, "geglu"), (13, 4096, 16384, "swiglu")])
-def test_skinny_split_k(gpu, oracle_mod, M, N, K, act):
-    # one token block, <= 128 row groups and K >= 64 steps of 128: two workgroups
-    # per group split K and the last to arrive adds the partials (ticket
-    # counters in the workspace header)
+def test_skinny_long_k(gpu, oracle_mod, M, N, K, act):
+    # one token block, <= 128 row groups and K >= 64 steps of 128: one
+    # workgroup (or two row halves) per group streams the whole of K
     from instinctflash_amd import _lib
     from instinctflash_amd.kernels import fp8 as F, pack_glu
     glu = act in ("geglu", "swiglu")
-    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) > 1024
+    assert _lib.load().ifx_fp8_linear_workspace_size(M, N, K, _lib.EPI_GEGLU if glu else 0) == 0
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
     n_out = N // 2 if glu else N
     res = torch.randn((M, n_out), generator=g).to(torch.bfloat16)
     w = pack_glu(fw) if glu else fw
-    o32, o16 = _check(gpu, oracle_mod, qa, sa, w, f"skinny split {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
-    # repeated calls: bit-identical (fixed slice order) and the counters return to zero
+    o32, o16 = _check(gpu, oracle_mod, qa, sa, w, f"skinny long K {M}x{N}x{K}", ref_w=fw, act=act, residual=res)
+    # repeated calls: bit-identical (fixed slice order), the workspace
+    # overwritten with a nonzero pattern in between
     for _ in range(3):
+        for ws in F._WORKSPACES.values():
+            ws.fill_(0xA5)
         again = F.linear(qa, sa, w, act=act, residual=res.to(gpu), out_dtype=torch.float32)
         assert torch.equal(again.view(torch.int32), o32.view(torch.int32))
-    torch.cuda.synchronize()
-    for ws in F._WORKSPACES.values():
-        assert int(ws[:1024].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
     # in place: out aliases the residual
     r = res.to(gpu).clone()
     F.linear(qa, sa, w, out=r, act=act, residual=r)

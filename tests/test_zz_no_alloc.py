@@ -2,8 +2,9 @@
 against ifx_quant_linear (caller workspace), through the C ABI: bit-identical
 outputs and scales on two calls in a row, the second with a smaller input,
 for the large-M path (split K with its partials in the scratch), the skinny
-path with its split-K ticket header, and per-tensor scaling; a call that
-needs more than the scratch is rejected before anything is launched."""
+path (long K, GLU), and per-tensor scaling; a call that needs more than the
+scratch is rejected before anything is launched. The caller workspace is
+filled with a nonzero pattern first: no part of it needs initialising."""
 import ctypes
 
 import pytest
@@ -37,7 +38,7 @@ def _call(lib, fn, x, fw, out, flags, mode, res, a_scale, ws=None):
     # (M1, M2, N, K, flags, scale mode)
     ("large split-K +res", 1024, 300, 2048, 11008, "res", "row"),
     ("large GELU", 512, 129, 4096, 2048, "gelu", "row"),
-    ("skinny split-K", 16, 8, 1024, 16384, None, "row"),
+    ("skinny long K", 16, 8, 1024, 16384, None, "row"),
     ("skinny GeGLU", 50, 16, 4096, 1024, "geglu", "row"),
     ("per tensor", 256, 64, 1536, 1536, None, "tensor"),
 ])
@@ -58,7 +59,7 @@ def test_noalloc_matches_workspace_call(gpu, case):
         ns = 1 if mode == "tensor" else M
         nbytes = lib.ifx_quant_linear_workspace_size(M, N, K, flags, smode)
         assert 0 < nbytes <= lib.ifx_quant_linear_noalloc_max_bytes()
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        ws = torch.full((nbytes,), 0xA5, dtype=torch.uint8, device=gpu)
         o_ref = torch.full((M, n_out), float("nan"), dtype=torch.bfloat16, device=gpu)
         o_na = torch.full_like(o_ref, -1.0)
         s_ref = torch.empty(ns, device=gpu)
