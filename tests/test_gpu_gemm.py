@@ -167,7 +167,10 @@ def test_wide_tile_k_loop_edges(gpu, oracle_mod, M, N, K, act):
     # loop has a prologue of two stages, a main part that issues the stage two
     # ahead and a tail of up to two stages without DMA; K of 1..5 stages and
     # 8 stages exercises every split of the three, ragged M and N clamp the
-    # DMA rows of the last tiles, GLU weights included
+    # DMA rows of the last tiles, GLU weights included. The ragged last token
+    # tiles also run the K-loop forms that skip token fragments past M: half
+    # of a wave's fragments (4112, 3000, 2100, 8100, 5000, 777) or none (the
+    # second token wave of 4112, 2100, 777)
     from instinctflash_amd.kernels import pack_glu
     qa, sa, fw, g = _make(gpu, M, N, K, seed=M + N + K, bias=True)
     glu = act in ("geglu", "swiglu")
