@@ -30,10 +30,9 @@
 //    register-staged double-buffered LDS tiles (16-byte chunks XOR-swizzled by
 //    row), epilogue from registers.
 //  * gemm_skinny (M <= 64): bound by the weight stream. A workgroup owns 16 (32
-//    for GLU) weight rows and a K slice; its waves split the slice, stream
-//    weight fragments straight from HBM into MFMA registers, and add their
-//    partial sums in LDS in a fixed order; slices of one row group are added
-//    by the last workgroup to arrive (deterministic, no waiting).
+//    for GLU) weight rows and the whole of K; its waves split the K steps,
+//    stream weight fragments straight from HBM into MFMA registers, and add
+//    their partial sums in LDS in a fixed order (deterministic).
 
 #include <algorithm>
 #include <mutex>
@@ -1281,11 +1280,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(const uint8_t* __restr
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t groups = e.N / (16 * NBW);
   // RH > 1: RH workgroups split the group's 16 weight rows (16 / RH each)
   const int rh = RH == 1 ? 0 : static_cast<int>(blockIdx.x % RH);
-  const int64_t bx = static_cast<int64_t>(blockIdx.x) / RH;
-  const int64_t grp = bx;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) / RH;  // row group
   const int64_t nrow0 = grp * (16 * NBW);
   const int frow = lane & 15;
   const int g = lane >> 4;
