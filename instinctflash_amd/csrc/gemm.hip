@@ -1602,8 +1602,10 @@ inline bool big_path(int64_t M, int64_t K) { return M > kSkinnyMaxM && K % kBigK
 //    stages), 128-byte stages, plus split K. 816 x 2048 x 16384: 44.1 us with 8
 //    waves, 42.8 pipelined with two stages, 41.0 with three; with the weights
 //    streamed from HBM 52.0 -> 42.4 us (two -> three stages), 1024 x 2048 x 11008
-//    44.2 -> 39.3 us. (44 us with 4 waves of 128 x 64 and 64-byte stages, 67 us
-//    for small tiles without a split.)
+//    44.2 -> 39.3 us. (44 us with 4 waves of 128 x 64 and 64-byte stages; the
+//    64 x 128 / 32 x 128 tiles without a split, re-measured on the current
+//    kernels: 1024 x 2048 x 11008 44.3 against 40.2 us, 816 x 2048 x 16384 56-60
+//    against 43-45 us.)
 enum class BigCfg { kWide, kWide192, kSmall, kSmall32, kNarrow };
 
 inline BigCfg pick_big(int64_t M, int64_t N, int64_t K, bool glu) {
