@@ -310,8 +310,10 @@ def test_contract_errors(gpu):
 
 def test_workspace_reuse_across_shapes(gpu, oracle_mod):
     # Regression: calls with different plans share one workspace per stream,
-    # whatever an earlier call left in it.
-    seq = [(16, 64, 4096), (16, 1536, 6144), (64, 256, 2048), (1, 512, 8192), (16, 1536, 6144), (50, 96, 4096)]
+    # whatever an earlier call left in it (large-M split-K calls of 32 and 8
+    # slices between skinny calls, which need none).
+    seq = [(16, 64, 4096), (100, 256, 16384), (16, 1536, 6144), (300, 512, 4736), (64, 256, 2048),
+           (100, 256, 16384), (1, 512, 8192), (50, 96, 4096)]
     for i, (M, N, K) in enumerate(seq):
         qa, sa, fw, _ = _make(gpu, M, N, K, seed=100 + i)
         from instinctflash_amd.kernels import linear
